@@ -1,0 +1,129 @@
+// Device helpers shared by the gfx950 kernels: bf16 conversion, MFMA wrappers,
+// cross-lane reductions and the QK-RMSNorm + RoPE row transform.
+//
+// Lane layout used throughout ("row-quad" layout): a wavefront of 64 lanes holds 16
+// rows of head_dim bf16 values. Lane l serves row n = l % 16 and, for every k-step
+// t < head_dim / 32, the 8 channels d = 32 t + 8 g + j (j < 8) with g = l / 16. This
+// is the operand layout of v_mfma_f32_16x16x32_bf16 (A: row = lane % 16; B: column
+// = lane % 16; both take 8 consecutive reduction indices per lane), so a row loaded
+// this way is directly an MFMA operand, and a row's sum of squares is a lane-local
+// sum followed by two cross-lane steps (xor 16, xor 32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fm {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// float32 -> bf16, round to nearest even: gfx950's v_cvt_pk_bf16_f32 (two values per
+// instruction).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float round_bf16(float f) { return (float)(__bf16)f; }
+
+// D(16x16 f32) += A(16x32 bf16) * B(32x16 bf16); operands as 4 packed dwords.
+__device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+// D(16x16 f32) += A(16x16 bf16) * B(16x16 bf16); operands as 2 packed dwords.
+__device__ __forceinline__ f32x4_t mfma_16x16x16(u32x2_t a, u32x2_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, a),
+                                                    __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
+// Reductions over the four lanes l, l^16, l^32, l^48 (the 4 groups of one row).
+__device__ __forceinline__ float sum_over_groups(float v) {
+  v += xor_shfl(v, 16);
+  v += xor_shfl(v, 32);
+  return v;
+}
+__device__ __forceinline__ float max_over_groups(float v) {
+  v = fmaxf(v, xor_shfl(v, 16));
+  v = fmaxf(v, xor_shfl(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ u32x4_t load16(const void *p) {
+  return *reinterpret_cast<const u32x4_t *>(p);
+}
+__device__ __forceinline__ void store16(void *p, u32x4_t v) { *reinterpret_cast<u32x4_t *>(p) = v; }
+
+// The rotary table of the kernels: cos/sin of pair i at row r.
+struct Rope {
+  const float *cos;
+  const float *sin;
+  int64_t row_stride;
+  int64_t pair_stride;
+  int64_t rows;  // > 0: clamp the row into [0, rows)
+};
+
+__device__ __forceinline__ int64_t clamp_row(const Rope &rope, int64_t r) {
+  if (rope.rows > 0) r = r < 0 ? 0 : (r >= rope.rows ? rope.rows - 1 : r);
+  return r;
+}
+
+// RMSNorm (scale rounded to bf16 before the multiply, product rounded to bf16) then
+// interleaved-pair RoPE (fp32 rotate of the bf16 normed values, rounded to bf16) of one
+// row held in the row-quad layout: x[t] holds channels 32 t + 8 g + (0..7). Every lane
+// of the wavefront must call this (the row reduction crosses lane groups). The
+// arithmetic is spelled with explicit round-to-nearest operations so that every
+// caller computes bit-identical values:
+//   r  = 1 / sqrt(sum(x^2) / D + eps)
+//   y  = bf16(x * bf16(w * r))
+//   e' = bf16(e c - o s),  o' = bf16(o c + e s)       (each product rounded)
+// Follows flashmap/modeling_flashmap.py:61-66,79-80 and flashmap/vllm/kernels.py:84-98.
+template <int D>
+__device__ __forceinline__ void norm_rope_row(u32x4_t (&x)[D / 32], const float *__restrict__ w,
+                                              float eps, const Rope &rope, int64_t rope_row,
+                                              int g) {
+  constexpr int KT = D / 32;
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float e = bf16_lo(x[t][q]), o = bf16_hi(x[t][q]);
+      ss = __fadd_rn(ss, __fmul_rn(e, e));
+      ss = __fadd_rn(ss, __fmul_rn(o, o));
+    }
+  }
+  ss = __fadd_rn(ss, xor_shfl(ss, 16));
+  ss = __fadd_rn(ss, xor_shfl(ss, 32));
+  const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+  const float *cs = rope.cos + rope_row * rope.row_stride;
+  const float *sn = rope.sin + rope_row * rope.row_stride;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int d = 32 * t + 8 * g + 2 * q;
+      const float se = round_bf16(__fmul_rn(w[d], r));
+      const float so = round_bf16(__fmul_rn(w[d + 1], r));
+      const float e = round_bf16(__fmul_rn(bf16_lo(x[t][q]), se));
+      const float o = round_bf16(__fmul_rn(bf16_hi(x[t][q]), so));
+      const float c = cs[(d >> 1) * rope.pair_stride];
+      const float s = sn[(d >> 1) * rope.pair_stride];
+      const float e2 = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s));
+      const float o2 = __fadd_rn(__fmul_rn(o, c), __fmul_rn(e, s));
+      x[t][q] = pack_bf16x2(e2, o2);
+    }
+  }
+}
+
+}  // namespace fm

@@ -1,0 +1,478 @@
+"""Torch-facing wrappers of the gfx950 kernels (``include/flashmap_amd.h``).
+
+Every function takes CUDA (ROCm) tensors, checks the contract the kernels rely on
+(dtype, alignment, strides), and enqueues the kernel on torch's current stream. The
+wrappers allocate only their outputs and, outside graph capture, the persistent
+split-KV workspace. There is no other code path: without the built library every
+call raises.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _native
+from ._native import call
+
+__all__ = [
+    "Rope",
+    "attention_plan",
+    "block_attention_contig",
+    "block_attention_paged",
+    "block_attention_token_paged",
+    "block_self_attention",
+    "rms_norm_rope",
+    "rope_from_cat",
+    "rope_from_split",
+    "rope_from_table",
+    "workspace_for",
+    "write_context_kv",
+    "write_context_kv_pool",
+]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check_cuda(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"flashmap_amd kernels run on the GPU; got a tensor on {t.device}")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"tensors on different devices: {device} and {t.device}")
+    return device
+
+
+def _bf16_rows(x: torch.Tensor, name: str) -> torch.Tensor:
+    """``x`` as bf16 with unit channel stride, 16-byte aligned rows (copied if needed)."""
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {x.dtype}")
+    ok = x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:-1])
+    return x if ok else x.contiguous()
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.float32 and t.is_contiguous()) else t.float().contiguous()
+
+
+def _i64(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.int64 and t.is_contiguous()) else t.to(torch.int64).contiguous()
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
+
+
+# ---------------------------------------------------------------------------- rope
+
+
+@dataclass(frozen=True)
+class Rope:
+    """A float32 rotary table as the kernels read it: cos/sin of pair ``i`` at row ``r``
+    are ``cos[r * row_stride + i * pair_stride]`` (same for ``sin``)."""
+
+    cos: torch.Tensor
+    sin_ptr: int
+    row_stride: int
+    pair_stride: int
+    rows: int
+    keep: tuple = ()
+
+    def args(self) -> list:
+        return [self.cos.data_ptr(), self.sin_ptr, self.row_stride, self.pair_stride, self.rows]
+
+
+def rope_from_table(cos_sin: torch.Tensor) -> Rope:
+    """vLLM's ``rope_table`` / SGLang's ``rope_freqs``: ``(..., D/2, 2)`` float32 with
+    (cos, sin) interleaved per pair (flashmap/vllm/kernels.py:26-33,
+    flashmap/sglang/model.py:116-123). Rows are the leading dims flattened."""
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.shape[-1] != 2:
+        raise ValueError("rotary table must be contiguous float32 (..., head_dim/2, 2)")
+    half = cos_sin.shape[-2]
+    return Rope(cos_sin, cos_sin.data_ptr() + 4, 2 * half, 2, max(cos_sin.numel() // (2 * half), 1), (cos_sin,))
+
+
+def rope_from_split(cos: torch.Tensor, sin: torch.Tensor) -> Rope:
+    """transformers' ``rope_tables``: separate ``cos`` and ``sin`` ``(..., D/2)``
+    (flashmap/modeling_flashmap.py:53-58)."""
+    cos, sin = _f32(cos), _f32(sin)
+    half = cos.shape[-1]
+    return Rope(cos, sin.data_ptr(), half, 1, max(cos.numel() // half, 1), (cos, sin))
+
+
+def rope_from_cat(table: torch.Tensor) -> Rope:
+    """SGLang's writer table ``(P, D)`` = ``[cos(D/2) | sin(D/2)]`` per row
+    (flashmap/sglang/model.py:814-817)."""
+    if table.dtype != torch.float32 or not table.is_contiguous():
+        raise ValueError("rotary table must be contiguous float32 (P, head_dim)")
+    d = table.shape[-1]
+    return Rope(table, table.data_ptr() + 4 * (d // 2), d, 1, table.numel() // d, (table,))
+
+
+# ------------------------------------------------------------------------ prologue
+
+
+def rms_norm_rope(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    rope: Rope,
+    positions: torch.Tensor | None,
+    eps: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """QK-RMSNorm + interleaved RoPE of ``x (tokens, heads, head_dim)`` bf16: the rope
+    row of token ``t`` is ``positions[t]`` (or ``t`` without positions)."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be (tokens, heads, head_dim), got {tuple(x.shape)}")
+    _check_cuda(x, weight, rope.cos, positions)
+    x = _bf16_rows(x, "x")
+    tokens, heads, head_dim = x.shape
+    if out is None:
+        out = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=x.device)
+    if tokens == 0:
+        return out
+    weight = _f32(weight)
+    pos = None if positions is None else _i64(positions)
+    call(
+        "fm_rms_norm_rope",
+        x.data_ptr(), out.data_ptr(), tokens, heads, head_dim,
+        x.stride(0), x.stride(1), out.stride(0), out.stride(1),
+        weight.data_ptr(), *rope.args(), _ptr(pos), float(eps), _stream(x),
+    )
+    return out
+
+
+# ----------------------------------------------------------------------- attention
+
+
+class _WorkspacePool:
+    """One persistent split-KV workspace per device, grown outside graph capture.
+    A replaced buffer is kept alive, since captured graphs may still point at it."""
+
+    def __init__(self):
+        self.buffers: dict[torch.device, torch.Tensor] = {}
+        self.retired: list[torch.Tensor] = []
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        buf = self.buffers.get(device)
+        if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"the attention workspace ({nbytes} bytes) must grow outside graph capture: "
+                    "run the call once (warm-up) before capturing"
+                )
+            if buf is not None:
+                self.retired.append(buf)
+            size = max(nbytes, 1 << 20)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            self.buffers[device] = buf
+        return buf
+
+
+_WORKSPACES = _WorkspacePool()
+_WS_BYTES: dict[tuple, int] = {}
+
+
+def workspace_for(batch: int, max_seqlen_q: int, hq: int, hkv: int, head_dim: int, max_seqlen_k: int,
+                  device: torch.device) -> torch.Tensor:
+    """The device's persistent workspace, large enough for an attention call of these
+    sizes (fm_attn_workspace_bytes)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (batch, max_seqlen_q, hq, hkv, head_dim, max_seqlen_k, index)
+    nbytes = _WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = int(_native.lib().fm_attn_workspace_bytes(batch, max_seqlen_q, hq, hkv, head_dim, max_seqlen_k, index))
+        if nbytes == 0:
+            raise RuntimeError(f"fm_attn_workspace_bytes failed: {_native.last_error()}")
+        _WS_BYTES[key] = nbytes
+    return _WORKSPACES.get(torch.device("cuda", index), nbytes)
+
+
+def attention_plan(seqlens: torch.Tensor) -> torch.Tensor:
+    """The split-KV plan of one step (int32 ``(batch + 1,)``), shared by every layer that
+    attends with these context lengths; the analogue of FlashAttention's
+    ``get_scheduler_metadata`` (flashmap/vllm/model.py:967-989)."""
+    _check_cuda(seqlens)
+    seqlens = _i32(seqlens)
+    batch = seqlens.shape[0]
+    plan = torch.empty(batch + 1, dtype=torch.int32, device=seqlens.device)
+    call("fm_attn_plan", seqlens.data_ptr(), batch, plan.data_ptr(), _stream(seqlens))
+    return plan
+
+
+@dataclass
+class Prologue:
+    """Fused QK-RMSNorm + RoPE of the queries inside the attention kernel."""
+
+    weight: torch.Tensor
+    rope: Rope
+    positions: torch.Tensor | None
+    eps: float
+
+    def args(self) -> list:
+        w = _f32(self.weight)
+        self._keep = (w, None if self.positions is None else _i64(self.positions))
+        return [w.data_ptr(), *self.rope.args(), _ptr(self._keep[1]), float(self.eps)]
+
+
+_NO_PROLOGUE = [None, None, None, 0, 0, 0, None, 0.0]
+
+
+def _q_out(query: torch.Tensor, out: torch.Tensor | None, varlen: bool):
+    query = _bf16_rows(query, "query")
+    if out is None:
+        out = torch.empty(query.shape, dtype=torch.bfloat16, device=query.device)
+    if varlen:  # (tokens, heads, D)
+        qs = [0, query.stride(0), query.stride(1)]
+        os_ = [0, out.stride(0), out.stride(1)]
+    else:  # (batch, q_len, heads, D)
+        qs = [query.stride(0), query.stride(1), query.stride(2)]
+        os_ = [out.stride(0), out.stride(1), out.stride(2)]
+    return query, out, qs, os_
+
+
+def block_attention_contig(
+    query: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    softmax_scale: float | None = None,
+    seqlens_k: torch.Tensor | None = None,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Non-causal attention of ``query (B, T, Hq, D)`` onto ``keys``/``values`` ``(B, Hkv,
+    L, D)`` (FlashMapCache.context views; any strides with unit channel stride).
+    ``seqlens_k (B,)`` limits each sequence to its first positions (default all L)."""
+    _check_cuda(query, keys, values, seqlens_k)
+    batch, q_len, hq, d = query.shape
+    _, hkv, kv_len, _ = keys.shape
+    keys, values = _bf16_rows(keys, "keys"), _bf16_rows(values, "values")
+    query, out, qs, os_ = _q_out(query, out, varlen=False)
+    if batch == 0 or q_len == 0:
+        return out
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
+    sl = None if seqlens_k is None else _i32(seqlens_k)
+    ws = workspace_for(batch, q_len, hq, hkv, d, kv_len, query.device)
+    call(
+        "fm_block_attn_contig",
+        query.data_ptr(), *qs, out.data_ptr(), *os_, None,
+        keys.data_ptr(), keys.stride(0), keys.stride(1), keys.stride(2),
+        values.data_ptr(), values.stride(0), values.stride(1), values.stride(2),
+        _ptr(sl), kv_len, batch, q_len, hq, hkv, d, float(scale),
+        *(prologue.args() if prologue else _NO_PROLOGUE),
+        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
+def block_attention_paged(
+    query: torch.Tensor,
+    kv_cache: torch.Tensor,
+    cu_seqlens_q: torch.Tensor | None,
+    seqused_k: torch.Tensor,
+    block_table: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Non-causal attention of ``query (tokens, Hq, D)`` (rows of request ``b`` from
+    ``cu_seqlens_q``) onto vLLM's paged cache ``(num_blocks, Hkv, page, 2D)`` (K then V
+    in every token row), each request reading its first ``seqused_k[b]`` positions
+    through ``block_table`` (flashmap/vllm/model.py:93-134)."""
+    _check_cuda(query, kv_cache, cu_seqlens_q, seqused_k, block_table)
+    if kv_cache.dtype != torch.bfloat16:
+        raise TypeError(f"kv_cache must be bfloat16, got {kv_cache.dtype}")
+    tokens, hq, d = query.shape
+    num_blocks, hkv, page, two_d = kv_cache.shape
+    if two_d != 2 * d:
+        raise ValueError(f"kv_cache rows hold {two_d} values, expected 2 * {d}")
+    if kv_cache.stride(-1) != 1:
+        raise ValueError("kv_cache must have unit channel stride")
+    batch = seqused_k.shape[0]
+    query, out, qs, os_ = _q_out(query, out, varlen=True)
+    if batch == 0 or tokens == 0:
+        return out
+    cu = None if cu_seqlens_q is None else _i32(cu_seqlens_q)
+    if cu is None:
+        qs[0], os_[0] = max_seqlen_q * qs[1], max_seqlen_q * os_[1]
+    bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(-1) == 1) else _i32(block_table)
+    sk = _i32(seqused_k)
+    ws = workspace_for(batch, max_seqlen_q, hq, hkv, d, max_seqlen_k, query.device)
+    call(
+        "fm_block_attn_paged",
+        query.data_ptr(), *qs, out.data_ptr(), *os_, _ptr(cu),
+        kv_cache.data_ptr(), num_blocks, kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), d, page,
+        bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
+        hq, hkv, d, float(softmax_scale),
+        *(prologue.args() if prologue else _NO_PROLOGUE),
+        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
+def block_attention_token_paged(
+    query: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    page_table: torch.Tensor,
+    softmax_scale: float | None = None,
+    max_seqlen_k: int | None = None,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Non-causal attention of ``query (bs, q_len, Hq, D)`` onto SGLang's token pool
+    ``key_buffer``/``value_buffer (pool, Hkv, D)``: request ``b`` reads pool rows
+    ``page_table[b, :cache_seqlens[b]]`` (flashmap/sglang/model.py:127-146)."""
+    _check_cuda(query, key_buffer, value_buffer, cache_seqlens, page_table)
+    batch, q_len, hq, d = query.shape
+    pool, hkv, _ = key_buffer.shape
+    key_buffer, value_buffer = _bf16_rows(key_buffer, "key_buffer"), _bf16_rows(value_buffer, "value_buffer")
+    query, out, qs, os_ = _q_out(query, out, varlen=False)
+    if batch == 0 or q_len == 0:
+        return out
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
+    pt = page_table if (page_table.dtype == torch.int32 and page_table.stride(-1) == 1) else _i32(page_table)
+    sl = _i32(cache_seqlens)
+    max_k = pt.shape[1] if max_seqlen_k is None else max_seqlen_k
+    ws = workspace_for(batch, q_len, hq, hkv, d, max_k, query.device)
+    call(
+        "fm_block_attn_token_paged",
+        query.data_ptr(), *qs, out.data_ptr(), *os_, None,
+        key_buffer.data_ptr(), value_buffer.data_ptr(), pool,
+        key_buffer.stride(0), key_buffer.stride(1), value_buffer.stride(0), value_buffer.stride(1),
+        pt.data_ptr(), pt.stride(0), pt.shape[1], sl.data_ptr(), batch, q_len, max_k,
+        hq, hkv, d, float(scale),
+        *(prologue.args() if prologue else _NO_PROLOGUE),
+        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
+# ------------------------------------------------------------------ self-attention
+
+
+def block_self_attention(
+    qkv: torch.Tensor,
+    q_norm: torch.Tensor,
+    k_norm: torch.Tensor,
+    rope: Rope,
+    positions: torch.Tensor | None,
+    eps: float,
+    softmax_scale: float | None = None,
+) -> torch.Tensor:
+    """Unmasked attention within each block of ``qkv (blocks, T, 3, heads, D)`` after
+    q/k RMSNorm + RoPE; returns ``(blocks, T, heads, D)`` bf16."""
+    _check_cuda(qkv, q_norm, k_norm, rope.cos, positions)
+    if qkv.dtype != torch.bfloat16:
+        raise TypeError(f"qkv must be bfloat16, got {qkv.dtype}")
+    qkv = qkv.contiguous()
+    blocks, t, three, heads, d = qkv.shape
+    if three != 3:
+        raise ValueError(f"qkv must be (blocks, T, 3, heads, head_dim), got {tuple(qkv.shape)}")
+    out = torch.empty((blocks, t, heads, d), dtype=torch.bfloat16, device=qkv.device)
+    if blocks == 0:
+        return out
+    qn, kn = _f32(q_norm), _f32(k_norm)
+    pos = None if positions is None else _i64(positions)
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
+    call(
+        "fm_block_self_attention",
+        qkv.data_ptr(), out.data_ptr(), blocks, t, heads, d, qn.data_ptr(), kn.data_ptr(),
+        *rope.args(), _ptr(pos), float(eps), float(scale), _stream(qkv),
+    )
+    return out
+
+
+# ------------------------------------------------------------------------ writers
+
+
+def write_context_kv(
+    kv: torch.Tensor,
+    positions: torch.Tensor,
+    slots: torch.Tensor,
+    k_norm: torch.Tensor,
+    rope: Rope,
+    cache_ptrs: torch.Tensor,
+    cache_strides: tuple[int, int, int, int],
+    block_size: int,
+    eps: float,
+    heads_per_cache: int | None = None,
+) -> None:
+    """k-norm + RoPE + store of ``kv (tokens, layers, 2, heads, D)`` into vLLM-layout
+    bf16 caches at ``slots`` (negative = skip); see fm_write_context_kv."""
+    _check_cuda(kv, positions, slots, k_norm, cache_ptrs)
+    if kv.dtype != torch.bfloat16:
+        raise TypeError(f"kv must be bfloat16, got {kv.dtype}")
+    kv = kv.contiguous()
+    tokens, layers, _, heads, d = kv.shape
+    if tokens == 0:
+        return
+    hpc = heads_per_cache or heads
+    if cache_ptrs.numel() * hpc < layers * heads:
+        raise ValueError(f"{cache_ptrs.numel()} caches of {hpc} heads cannot hold {layers} x {heads} heads")
+    sb, sh, st, voff = cache_strides
+    kn = _f32(k_norm)
+    call(
+        "fm_write_context_kv",
+        kv.data_ptr(), tokens, layers, heads, d, _i64(positions).data_ptr(), _i64(slots).data_ptr(),
+        kn.data_ptr(), *rope.args(), _i64(cache_ptrs).data_ptr(), cache_ptrs.numel(), hpc,
+        sb, sh, st, voff, block_size, float(eps), _stream(kv),
+    )
+
+
+def write_context_kv_pool(
+    kv: torch.Tensor,
+    meta: torch.Tensor,
+    k_norm_weights: torch.Tensor,
+    rope: Rope,
+    positions: torch.Tensor,
+    locs: torch.Tensor,
+    num_layers: int,
+    kv_size: int,
+    head_dim: int,
+    eps: float,
+    commit_lens: torch.Tensor | None = None,
+    locs_row_width: int | None = None,
+) -> None:
+    """k-norm + RoPE + store of ``kv (tokens, layers * 2 * kv_size)`` into SGLang pools
+    described by ``meta (layers, 4)``; see fm_write_context_kv_pool."""
+    _check_cuda(kv, meta, k_norm_weights, positions, locs, commit_lens)
+    if kv.dtype != torch.bfloat16:
+        raise TypeError(f"kv must be bfloat16, got {kv.dtype}")
+    kv = kv.contiguous()
+    tokens = kv.shape[0]
+    if tokens == 0:
+        return
+    heads = kv_size // head_dim
+    if kv.numel() != tokens * num_layers * 2 * kv_size:
+        raise ValueError("kv must be (tokens, layers * 2 * kv_size)")
+    cl = None if commit_lens is None else _i32(commit_lens)
+    call(
+        "fm_write_context_kv_pool",
+        kv.data_ptr(), tokens, num_layers, heads, head_dim, _i64(meta).data_ptr(),
+        _f32(k_norm_weights).data_ptr(), *rope.args(), _i64(positions).data_ptr(), _i64(locs).data_ptr(),
+        _ptr(cl), int(locs_row_width or 0), float(eps), _stream(kv),
+    )
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

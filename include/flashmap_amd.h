@@ -1,0 +1,235 @@
+/*
+ * flashmap_amd.h - C ABI of the MI355X (gfx950) kernels for the FlashMap drafter's
+ * cross-attention hot path: the per-layer QK-RMSNorm + RoPE prologue, the block
+ * attention of K draft slots onto the target's context keys/values (contiguous,
+ * block-paged and token-paged KV), the in-block self-attention and the context-KV
+ * writers that produce the paged layouts.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers unless stated; tensors are bf16 (passed as void*),
+ *     float32 (float*) or integer as typed. Strides are in ELEMENTS, not bytes.
+ *   - Nothing is allocated and nothing synchronizes: work is enqueued on `stream`
+ *     (a hipStream_t passed as void*; NULL = the legacy default stream).
+ *   - Return FM_OK (0) or an FM_ERR_* code; fm_last_error() then describes the
+ *     failure (thread-local string owned by the library).
+ *   - RoPE rotates interleaved channel pairs (2i, 2i+1). A rotary table is given as
+ *     two float32 arrays: cos and sin of pair i at table row r are
+ *       rope_cos[r * rope_row_stride + i * rope_pair_stride]   (same for rope_sin).
+ *     The row of token t is positions[t] when `positions` is non-NULL, else t.
+ *     rope_rows (> 0) bounds the row index (rows are clamped into [0, rope_rows)).
+ *   - RMSNorm is x * bf16(w * rsqrt(mean(x^2) + eps)), the product rounded to bf16.
+ */
+#ifndef FLASHMAP_AMD_H
+#define FLASHMAP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FM_OK = 0,
+  FM_ERR_INVALID = 1,     /* bad shape, stride, dtype contract or NULL pointer */
+  FM_ERR_UNSUPPORTED = 2, /* a shape the kernels do not implement (e.g. head_dim) */
+  FM_ERR_WORKSPACE = 3,   /* workspace missing or smaller than fm_*_workspace_bytes */
+  FM_ERR_HIP = 4          /* a HIP runtime call failed (launch, attribute query) */
+};
+
+#define FM_ABI_VERSION 1
+
+/* Library metadata and errors. No reference counterpart (the reference raises Python
+ * exceptions: assert / ValueError in flashmap/vllm/kernels.py:51,112,341-342). */
+const char *fm_last_error(void);
+int fm_abi_version(void);
+/* Compute units of `device` (the split-KV planner sizes its grid from it). */
+int fm_device_cus(int device, int *num_cus);
+
+/* ---------------------------------------------------------------------------------
+ * a2/a3  Q prologue: RMSNorm of every (token, head) row of x, then RoPE.
+ * Replaces flashmap_vllm::rms_norm_rope (flashmap/vllm/kernels.py:101-124; table
+ * rows gathered at positions) and flashmap_sglang::rms_norm_rope
+ * (flashmap/sglang/kernels.py:171-189; one table row per token, positions = NULL);
+ * same math as FlashMapAttention's q_norm + apply_rope
+ * (flashmap/modeling_flashmap.py:61-80,145). x and out: (tokens, heads, head_dim)
+ * bf16 with the given token/head strides (unit stride inside a head).
+ * head_dim in {64, 128}.
+ */
+int fm_rms_norm_rope(const void *x, void *out, int64_t tokens, int32_t heads, int32_t head_dim,
+                     int64_t x_stride_token, int64_t x_stride_head, int64_t out_stride_token,
+                     int64_t out_stride_head, const float *weight, const float *rope_cos,
+                     const float *rope_sin, int64_t rope_row_stride, int64_t rope_pair_stride,
+                     int64_t rope_rows, const int64_t *positions, float eps, void *stream);
+
+/* ---------------------------------------------------------------------------------
+ * a5/a6/a7  Block attention: for each sequence b, its q_len(b) draft rows of every
+ * query head attend, non-causally, to the first seqlen(b) context positions:
+ *   out = softmax(Q K^T * softmax_scale) V
+ * in fp32 with P rounded to bf16 before P.V, output rounded to bf16 once.
+ * GQA: query head hq attends to KV head hq / (num_q_heads / num_kv_heads).
+ *
+ * Query / output rows: token t of sequence b is row cu_seqlens_q[b] + t when
+ * cu_seqlens_q is non-NULL (varlen, strides *_stride_token / *_stride_head), else
+ * b * *_stride_batch + t * *_stride_token. q_len(b) = cu_seqlens_q[b+1] -
+ * cu_seqlens_q[b] (<= max_seqlen_q) or max_seqlen_q.
+ *
+ * Optional fused Q prologue: with q_norm_weight non-NULL the kernel reads the
+ * pre-norm projection q and applies fm_rms_norm_rope's math itself (the rope row of
+ * query token row i is q_positions[i] or i, i being the varlen row index
+ * cu_seqlens_q[b] + t, or b * max_seqlen_q + t without cu_seqlens_q).
+ *
+ * Split-KV: the context of all sequences is cut into equal shares over a persistent
+ * grid (one share per workgroup); a sequence cut across shares is merged by a second
+ * fp32 log-sum-exp pass. `plan` is fm_attn_plan's output for this step (it depends
+ * only on the context lengths, so every layer of a step may share it); NULL plans
+ * inside the call, in the workspace. `workspace` must hold
+ * fm_attn_workspace_bytes(...) bytes for the same arguments; it is scratch that
+ * concurrent calls must not share.
+ * head_dim in {64, 128}; num_q_heads % num_kv_heads == 0.
+ * A sequence with seqlen(b) == 0 gets zeros (vLLM's seqused_k = 0 rows).
+ * ------------------------------------------------------------------------------ */
+
+/* Bytes of the plan buffer for `batch` sequences. */
+size_t fm_attn_plan_bytes(int32_t batch);
+/* Writes the step's plan from seqlens (batch,) int32 into `plan` (device, int32).
+ * Replaces get_scheduler_metadata (flashmap/vllm/model.py:967-989,
+ * flashmap/sglang/model.py:189-204). */
+int fm_attn_plan(const int32_t *seqlens, int32_t batch, int32_t *plan, void *stream);
+
+/* Workspace bytes an attention call with these sizes needs on `device`. */
+size_t fm_attn_workspace_bytes(int32_t batch, int32_t max_seqlen_q, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
+                               int device);
+
+/* a5: contiguous KV, the FlashMapCache layout (flashmap/modeling_flashmap.py:195-219):
+ * K and V views (batch, kv_heads, positions, head_dim) with arbitrary strides.
+ * seqlens_k NULL: every sequence attends to kv_len positions (FlashMapCache.context(end)).
+ * Replaces F.scaled_dot_product_attention in FlashMapAttention.forward
+ * (flashmap/modeling_flashmap.py:144-147). */
+int fm_block_attn_contig(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *k, int64_t k_stride_batch, int64_t k_stride_head,
+    int64_t k_stride_pos, const void *v, int64_t v_stride_batch, int64_t v_stride_head,
+    int64_t v_stride_pos, const int32_t *seqlens_k, int32_t kv_len, int32_t batch,
+    int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* a6: block-paged KV, vLLM's FlashAttention cache as the FlashMap plugin views it
+ * ((num_blocks, kv_heads, page_size, 2 * head_dim): K then V in every token row;
+ * flashmap/vllm/model.py:93-139,707-733). Position p of sequence b lives in page
+ * block_table[b * block_table_stride + p / page_size] at token p % page_size:
+ *   K = kv_cache + page * stride_block + head * stride_head + (p % page) * stride_token
+ *   V = K + v_offset.
+ * Page ids are clamped into [0, num_blocks), block-table columns into
+ * [0, block_table_width). Replaces flashmap_vllm::paged_cross_attention
+ * (flashmap/vllm/model.py:93-134, i.e. vllm_flash_attn.flash_attn_varlen_func with
+ * causal=False). */
+int fm_block_attn_paged(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *kv_cache, int64_t num_blocks, int64_t stride_block,
+    int64_t stride_head, int64_t stride_token, int64_t v_offset, int32_t page_size,
+    const int32_t *block_table, int64_t block_table_stride, int64_t block_table_width,
+    const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+    const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* a7: token-paged KV, SGLang's pool ((pool_size, kv_heads, head_dim) key and value
+ * buffers): position p of sequence b is pool row page_table[b * page_table_stride + p]
+ * (flashmap/sglang/model.py:127-151, 785-786, 861-864). Pool rows are clamped into
+ * [0, pool_size). Replaces flashmap_sglang::paged_cross_attention
+ * (flashmap/sglang/model.py:127-146, i.e. sgl_kernel flash_attn_with_kvcache with
+ * page size 1, causal=False). */
+int fm_block_attn_token_paged(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *key_buffer, const void *value_buffer,
+    int64_t pool_size, int64_t k_stride_slot, int64_t k_stride_head, int64_t v_stride_slot,
+    int64_t v_stride_head, const int32_t *page_table, int64_t page_table_stride,
+    int64_t page_table_width, const int32_t *cache_seqlens, int32_t batch, int32_t max_seqlen_q,
+    int32_t max_seqlen_k, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------------
+ * a8  Block self-attention with fused q/k RMSNorm + RoPE: qkv (blocks, block_size,
+ * 3, heads, head_dim) bf16 contiguous -> out (blocks, block_size, heads, head_dim)
+ * bf16 contiguous (the same bytes as vLLM's (blocks * block_size, heads * head_dim)).
+ * Rope row of slot token i (= block * block_size + t) is positions[i] or i.
+ * block_size <= 16, head_dim in {64, 128}. Replaces flashmap_vllm::block_self_attention
+ * (flashmap/vllm/kernels.py:194-232) and flashmap_sglang::block_self_attention
+ * (flashmap/sglang/kernels.py:84-120).
+ */
+int fm_block_self_attention(const void *qkv, void *out, int64_t blocks, int32_t block_size,
+                            int32_t heads, int32_t head_dim, const float *q_norm_weight,
+                            const float *k_norm_weight, const float *rope_cos,
+                            const float *rope_sin, int64_t rope_row_stride,
+                            int64_t rope_pair_stride, int64_t rope_rows,
+                            const int64_t *positions, float eps, float softmax_scale,
+                            void *stream);
+
+/* ---------------------------------------------------------------------------------
+ * a4  Context KV writers (the K side of the QK-norm prologue). Every layer's keys are
+ * k-normed (k_norm_weight row = layer, float32 (layers, head_dim)) and rotated at
+ * their context position, then stored as bf16 together with the values.
+ *
+ * fm_write_context_kv: kv (tokens, layers, 2, heads, head_dim) bf16 contiguous into
+ * vLLM-layout paged caches. Head h of layer l is global head gh = l * heads + h and
+ * lives in cache gh / heads_per_cache (device array cache_ptrs[num_caches] of data
+ * pointers) at cache head gh % heads_per_cache, token slot s = slots[t]:
+ *   K = cache + (s / page_size) * stride_block + head * stride_head
+ *       + (s % page_size) * stride_token,  V = K + v_offset.
+ * slots[t] < 0 skips token t. Replaces write_context_kv
+ * (flashmap/vllm/kernels.py:311-364) for bf16 caches.
+ */
+int fm_write_context_kv(const void *kv, int64_t tokens, int32_t layers, int32_t heads,
+                        int32_t head_dim, const int64_t *positions, const int64_t *slots,
+                        const float *k_norm_weight, const float *rope_cos, const float *rope_sin,
+                        int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+                        const int64_t *cache_ptrs, int32_t num_caches, int32_t heads_per_cache,
+                        int64_t stride_block, int64_t stride_head, int64_t stride_token,
+                        int64_t v_offset, int32_t page_size, float eps, void *stream);
+
+/* fm_write_context_kv_pool: kv (tokens, layers * 2 * heads * head_dim) bf16
+ * contiguous (per layer: keys of all heads, then values) into SGLang-layout pools.
+ * meta (layers, 4) int64 device array: key buffer pointer, value buffer pointer, key
+ * row stride, value row stride (elements); head h of a row at h * head_dim.
+ * locs[t] < 0 skips token t; with commit_lens non-NULL, token t is skipped when
+ * t % locs_row_width >= commit_lens[t / locs_row_width] (uncommitted verify columns).
+ * Replaces sglang's fused_kv_norm_rope_write as the plugin calls it
+ * (flashmap/sglang/model.py:746-766, is_neox_style=False) for bf16 pools, with the
+ * reference rounding (scale rounded to bf16 before the multiply).
+ */
+int fm_write_context_kv_pool(const void *kv, int64_t tokens, int32_t layers, int32_t heads,
+                             int32_t head_dim, const int64_t *meta, const float *k_norm_weight,
+                             const float *rope_cos, const float *rope_sin,
+                             int64_t rope_row_stride, int64_t rope_pair_stride,
+                             int64_t rope_rows, const int64_t *positions, const int64_t *locs,
+                             const int32_t *commit_lens, int64_t locs_row_width, float eps,
+                             void *stream);
+
+/* ---------------------------------------------------------------------------------
+ * Measurement hook. No reference counterpart: it lets a benchmark time the main
+ * split-KV attention kernel alone with HIP events on the stream it runs on, without
+ * changing the work any call does. While enabled, every attention call records an
+ * event pair around its main kernel; fm_profile_read synchronizes those events and
+ * returns the summed milliseconds and the number of launches, then clears them.
+ */
+int fm_profile_enable(int enable);
+int fm_profile_read(double *total_ms, int64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHMAP_AMD_H */

@@ -1,0 +1,294 @@
+"""CPU restatement of the reference drafter-attention math (torch on the CPU).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). Each function cites the reference
+lines it restates. Pinning (tests/test_oracle_*.py): closed forms, invariants and
+float64 brute force on tiny inputs; which check pins which function is listed in the
+functions' docstrings under "Pinned by".
+
+Numerics follow the reference modules:
+  * RMSNorm: ``x * to_dtype(w_f32 * rsqrt(mean(x_f32^2) + eps))``
+    (flashmap/modeling_flashmap.py:79-80);
+  * RoPE: interleaved pairs ``(2i, 2i+1)`` rotated in float32, rounded to x's dtype
+    (flashmap/modeling_flashmap.py:61-66);
+  * attention: non-causal ``softmax(q k^T * scale) v`` in float32, GQA by repeating
+    each KV head over its group of query heads (the fp32 reference of
+    ``F.scaled_dot_product_attention`` at flashmap/modeling_flashmap.py:146).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+# ----------------------------------------------------------------------------- rope
+
+
+def inv_freq(head_dim: int, theta: float) -> torch.Tensor:
+    """``1 / theta ** (arange(0, D, 2) / D)`` in float32 (flashmap/modeling_flashmap.py:56).
+    Pinned by: closed form against float64 (test_oracle_rope)."""
+    return 1.0 / theta ** (torch.arange(0, head_dim, 2).float() / head_dim)
+
+
+def rope_tables(positions: torch.Tensor, head_dim: int, theta: float):
+    """``(cos, sin)`` each ``(B, T, 1, D/2)`` float32 at ``positions (B, T)``
+    (flashmap/modeling_flashmap.py:53-58). Pinned by: identity at position 0, pair-norm
+    preservation, relative-position invariance of q.k (test_oracle_rope)."""
+    angles = positions.float()[..., None, None] * inv_freq(head_dim, theta)
+    return angles.cos(), angles.sin()
+
+
+def rope_table(max_positions: int, head_dim: int, base: float) -> torch.Tensor:
+    """vLLM table ``(P, D/2, 2)`` of ``(cos, sin)`` (flashmap/vllm/kernels.py:26-33).
+    Pinned by: equality with rope_tables rows (test_oracle_rope)."""
+    angles = torch.arange(max_positions).float()[:, None] * inv_freq(head_dim, base)
+    return torch.stack([angles.cos(), angles.sin()], dim=-1).contiguous()
+
+
+def rope_freqs(positions: torch.Tensor, head_dim: int, theta: float) -> torch.Tensor:
+    """SGLang per-position table ``(..., D/2, 2)`` (flashmap/sglang/model.py:116-123).
+    Pinned by: equality with rope_table rows (test_oracle_rope)."""
+    angles = positions.float()[..., None] * inv_freq(head_dim, theta)
+    return torch.stack([angles.cos(), angles.sin()], dim=-1)
+
+
+def rope_cat_table(max_positions: int, head_dim: int, theta: float) -> torch.Tensor:
+    """SGLang writer table ``(P, D)``: ``[cos(D/2) | sin(D/2)]`` per row
+    (flashmap/sglang/model.py:814-817). Pinned by: equality with rope_table rows."""
+    freqs = rope_freqs(torch.arange(max_positions), head_dim, theta)
+    return torch.cat([freqs[..., 0], freqs[..., 1]], dim=-1).contiguous()
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate interleaved pairs ``(x[2i], x[2i+1])`` of ``x (..., D)`` by angles with
+    ``cos``/``sin`` broadcastable to ``(..., D/2)``, in float32, result in x's dtype
+    (flashmap/modeling_flashmap.py:61-66). Pinned by: a 2x2 rotation per pair checked
+    against float64 (test_oracle_rope)."""
+    x1, x2 = x.float().unflatten(-1, (-1, 2)).unbind(-1)
+    return torch.stack([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).flatten(-2).type_as(x)
+
+
+# -------------------------------------------------------------------------- norms
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``x * to_dtype(w_f32 * rsqrt(mean(x_f32^2) + eps))`` over the last dim
+    (flashmap/modeling_flashmap.py:69-80). Pinned by: float64 closed form with the
+    bf16 rounding points, unit RMS of the output at w = 1 (test_oracle_norm)."""
+    rms = torch.rsqrt(x.float().pow(2).mean(dim=-1, keepdim=True) + eps)
+    return x * (weight.float() * rms).to(x.dtype)
+
+
+def rms_norm_rope_vllm(x, weight, cos_sin, positions, eps):
+    """flashmap_vllm::rms_norm_rope on ``x (tokens, H, D)``: rope rows gathered at
+    ``positions`` of the ``(P, D/2, 2)`` table (flashmap/vllm/kernels.py:67-124).
+    Pinned by: composition of the pinned rms_norm and apply_rope (test_oracle_norm)."""
+    rows = cos_sin[positions.long()]  # (tokens, D/2, 2)
+    cos, sin = rows[..., 0][:, None, :], rows[..., 1][:, None, :]
+    return apply_rope(rms_norm(x, weight, eps), cos, sin)
+
+
+def rms_norm_rope_sglang(x, weight, freqs, eps):
+    """flashmap_sglang::rms_norm_rope on ``x (..., T, H, D)`` with one table row per
+    token ``freqs (..., T, D/2, 2)`` (flashmap/sglang/kernels.py:149-189)."""
+    cos, sin = freqs[..., 0].unsqueeze(-2), freqs[..., 1].unsqueeze(-2)
+    return apply_rope(rms_norm(x, weight, eps), cos, sin)
+
+
+# ---------------------------------------------------------------------- attention
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None) -> torch.Tensor:
+    """Non-causal ``softmax(q k^T * scale) v`` in float32 for ``q (..., Hq, T, D)`` and
+    ``k, v (..., Hkv, L, D)``; query head h reads KV head ``h // (Hq / Hkv)``
+    (flashmap/modeling_flashmap.py:146; the GQA convention of
+    flashmap/sglang/verify_attention.py:77-79). Returns float32 ``(..., Hq, T, D)``.
+    Pinned by: float64 brute force, rows of P sum to 1, one key -> v, key permutation
+    invariance, GQA == MHA on repeated KV (test_oracle_attention)."""
+    d = q.shape[-1]
+    scale = d ** -0.5 if scale is None else scale
+    hq, hkv = q.shape[-3], k.shape[-3]
+    if hq != hkv:
+        k = k.repeat_interleave(hq // hkv, dim=-3)
+        v = v.repeat_interleave(hq // hkv, dim=-3)
+    s = (q.float() @ k.float().transpose(-1, -2)) * scale
+    return s.softmax(dim=-1) @ v.float()
+
+
+def attention_lse(q, k, v, scale=None):
+    """``(out, lse)`` of :func:`attention` with lse the natural log-sum-exp of the
+    scaled scores per row; -inf (and out 0) for an empty key set. The partial a split
+    of the context hands to the merge (flashmap/sglang/verify_attention.py:172-181).
+    Pinned by: merge of splits == unsplit attention (test_oracle_attention)."""
+    d = q.shape[-1]
+    scale = d ** -0.5 if scale is None else scale
+    hq, hkv = q.shape[-3], k.shape[-3]
+    if hq != hkv:
+        k = k.repeat_interleave(hq // hkv, dim=-3)
+        v = v.repeat_interleave(hq // hkv, dim=-3)
+    if k.shape[-2] == 0:
+        shape = (*q.shape[:-1],)
+        return torch.zeros((*shape, v.shape[-1])), torch.full(shape, -math.inf)
+    s = (q.float() @ k.float().transpose(-1, -2)) * scale
+    lse = torch.logsumexp(s, dim=-1)
+    return (s - lse[..., None]).exp() @ v.float(), lse
+
+
+def lse_merge(outs: list[torch.Tensor], lses: list[torch.Tensor]) -> torch.Tensor:
+    """Merge split partials ``O = sum_s exp(lse_s - m) O_s / sum_s exp(lse_s - m)``,
+    skipping splits with lse = -inf (flashmap/sglang/verify_attention.py:184-233).
+    Pinned by: merge of splits == unsplit attention (test_oracle_attention)."""
+    lse = torch.stack(lses)
+    m = lse.max(dim=0).values
+    m = torch.where(torch.isinf(m), torch.zeros_like(m), m)
+    w = torch.exp(lse - m)  # exp(-inf) = 0 for empty splits
+    num = sum(wi[..., None] * oi for wi, oi in zip(w, outs))
+    den = w.sum(dim=0)
+    return num / torch.where(den > 0, den, torch.ones_like(den))[..., None]
+
+
+def block_attention_contig(query, keys, values, seqlens_k=None, scale=None):
+    """a5: ``query (B, T, Hq, D)`` onto FlashMapCache views ``keys/values (B, Hkv, L, D)``,
+    sequence b reading its first ``seqlens_k[b]`` positions (all L by default)
+    (flashmap/modeling_flashmap.py:144-147, 218-219). Returns float32 (B, T, Hq, D);
+    zeros for an empty context."""
+    b_, t_, hq, d = query.shape
+    out = torch.zeros((b_, t_, hq, d))
+    for b in range(b_):
+        n = keys.shape[2] if seqlens_k is None else int(seqlens_k[b])
+        if n <= 0:
+            continue
+        out[b] = attention(query[b].transpose(0, 1), keys[b, :, :n], values[b, :, :n], scale).transpose(0, 1)
+    return out
+
+
+# ----------------------------------------------------------------- paged layouts
+
+
+def vllm_gather_slots(block_table: np.ndarray, seqlen: int, page_size: int, b: int) -> np.ndarray:
+    """Physical (page, in-page token) of positions ``0..seqlen-1`` of request ``b``:
+    ``(block_table[b, p // page], p % page)`` (the block-table addressing of
+    flashmap/vllm/model.py:107-134). Pinned by: exact integer closed form checked
+    elementwise against a direct loop (test_oracle_layouts)."""
+    p = np.arange(seqlen)
+    return np.stack([block_table[b, p // page_size], p % page_size], axis=-1)
+
+
+def gather_vllm(kv_cache: torch.Tensor, block_table, seqlen: int, b: int):
+    """K and V ``(Hkv, seqlen, D)`` of request ``b`` from a vLLM cache
+    ``(num_blocks, Hkv, page, 2D)`` whose rows hold K then V
+    (flashmap/vllm/model.py:107-112: ``kv_cache.transpose(1, 2).split(D, -1)``)."""
+    d = kv_cache.shape[-1] // 2
+    page = kv_cache.shape[2]
+    idx = vllm_gather_slots(np.asarray(block_table), seqlen, page, b)
+    rows = kv_cache[torch.as_tensor(idx[:, 0]), :, torch.as_tensor(idx[:, 1])]  # (seqlen, Hkv, 2D)
+    return rows[..., :d].transpose(0, 1), rows[..., d:].transpose(0, 1)
+
+
+def block_attention_paged_vllm(query, kv_cache, cu_seqlens_q, seqused_k, block_table, scale=None):
+    """a6: flashmap_vllm::paged_cross_attention (flashmap/vllm/model.py:93-134):
+    request b's query rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` of ``query (tokens,
+    Hq, D)`` attend non-causally to its first ``seqused_k[b]`` paged positions.
+    Returns float32 (tokens, Hq, D), zeros for empty contexts."""
+    out = torch.zeros(query.shape)
+    bt = np.asarray(block_table)
+    for b in range(len(seqused_k)):
+        lo, hi = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+        n = int(seqused_k[b])
+        if n <= 0 or hi <= lo:
+            continue
+        k, v = gather_vllm(kv_cache, bt, n, b)
+        out[lo:hi] = attention(query[lo:hi].transpose(0, 1), k, v, scale).transpose(0, 1)
+    return out
+
+
+def block_attention_token_paged(query, key_buffer, value_buffer, cache_seqlens, page_table, scale=None):
+    """a7: flashmap_sglang::paged_cross_attention (flashmap/sglang/model.py:127-146):
+    request b (``query (bs, T, Hq, D)``) reads pool rows ``page_table[b, :cache_seqlens[b]]``
+    of ``key_buffer/value_buffer (pool, Hkv, D)``. Returns float32 (bs, T, Hq, D)."""
+    out = torch.zeros(query.shape)
+    for b in range(query.shape[0]):
+        n = int(cache_seqlens[b])
+        if n <= 0:
+            continue
+        rows = torch.as_tensor(np.asarray(page_table)[b, :n]).long()
+        k = key_buffer[rows].transpose(0, 1)
+        v = value_buffer[rows].transpose(0, 1)
+        out[b] = attention(query[b].transpose(0, 1), k, v, scale).transpose(0, 1)
+    return out
+
+
+# -------------------------------------------------------------- self-attention (a8)
+
+
+def block_self_attention(qkv, q_norm, k_norm, cos, sin, eps, scale=None):
+    """a8: q/k RMSNorm + RoPE then unmasked softmax attention within each block of
+    ``qkv (blocks, T, 3, H, D)``; ``cos/sin (blocks, T, D/2)`` per slot. Returns float32
+    (blocks, T, H, D) (flashmap/vllm/kernels.py:127-191, flashmap/sglang/kernels.py:18-75;
+    transformers: flashmap/modeling_flashmap.py:188). Pinned by: composition of pinned
+    rms_norm / apply_rope / attention."""
+    q, k, v = qkv.unbind(2)  # (blocks, T, H, D)
+    c, s = cos[:, :, None, :], sin[:, :, None, :]
+    q = apply_rope(rms_norm(q, q_norm, eps), c, s)
+    k = apply_rope(rms_norm(k, k_norm, eps), c, s)
+    return attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), scale).transpose(1, 2)
+
+
+# ------------------------------------------------------------------ writers (a4)
+
+
+def project_keys(k_rows, k_norm_w, cos, sin, eps):
+    """The K side of the prologue: ``apply_rope(k_norm(k))`` of ``k_rows (..., H, D)``
+    with ``cos/sin`` broadcastable to ``(..., 1, D/2)`` (flashmap/modeling_flashmap.py:139-142;
+    flashmap/vllm/kernels.py:276-290)."""
+    return apply_rope(rms_norm(k_rows, k_norm_w, eps), cos, sin)
+
+
+def write_context_kv_vllm(kv, positions, slots, k_norm, cos_sin, caches, block_size, eps, heads_per_cache=None):
+    """vLLM ``write_context_kv`` for bf16 caches (flashmap/vllm/kernels.py:235-364):
+    ``kv (tokens, L, 2, H, D)``; head h of layer l (global head l*H + h) goes to cache
+    ``g // HPC`` head ``g % HPC`` at slot ``slots[t]`` (skipped if negative); caches are
+    ``(num_blocks, HPC, page, 2D)`` tensors, updated in place. Pinned by: write then
+    gather round trip equals project_keys / v (test_oracle_layouts)."""
+    tokens, layers, _, heads, d = kv.shape
+    hpc = heads_per_cache or heads
+    rows = cos_sin[positions.long()]  # (tokens, D/2, 2)
+    cos, sin = rows[..., 0][:, None, :], rows[..., 1][:, None, :]
+    for t in range(tokens):
+        slot = int(slots[t])
+        if slot < 0:
+            continue
+        page, tok = divmod(slot, block_size)
+        for l in range(layers):
+            keys = project_keys(kv[t, l, 0][None], k_norm[l], cos[t:t + 1], sin[t:t + 1], eps)[0]
+            for h in range(heads):
+                g = l * heads + h
+                c, s = divmod(g, hpc)
+                caches[c][page, s, tok, :d] = keys[h]
+                caches[c][page, s, tok, d:] = kv[t, l, 1, h]
+
+
+def write_context_kv_pool(kv, k_bufs, v_bufs, k_norm, cos_sin_cat, positions, locs, num_layers, kv_size,
+                          head_dim, eps, commit_lens=None, locs_row_width=None):
+    """SGLang pool write (fused_kv_norm_rope_write as flashmap/sglang/model.py:746-766
+    calls it, interleaved RoPE; the reference's rounding of the norm, scale rounded to
+    bf16 first, flashmap/modeling_flashmap.py:79-80): ``kv (tokens, L*2*kv_size)``,
+    per layer keys then values; token t goes to pool row ``locs[t]`` unless negative or
+    past its request's ``commit_lens`` column."""
+    heads = kv_size // head_dim
+    half = head_dim // 2
+    rows = cos_sin_cat[positions.long()]
+    cos, sin = rows[:, None, :half], rows[:, None, half:]
+    for t in range(kv.shape[0]):
+        loc = int(locs[t])
+        if loc < 0:
+            continue
+        if commit_lens is not None and t % locs_row_width >= int(commit_lens[t // locs_row_width]):
+            continue
+        for l in range(num_layers):
+            base = l * 2 * kv_size
+            k = kv[t, base:base + kv_size].view(heads, head_dim)
+            v = kv[t, base + kv_size:base + 2 * kv_size].view(heads, head_dim)
+            k_bufs[l][loc] = project_keys(k[None], k_norm[l], cos[t:t + 1], sin[t:t + 1], eps)[0]
+            v_bufs[l][loc] = v

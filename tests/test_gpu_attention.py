@@ -1,0 +1,248 @@
+"""GPU parity of the block attention kernels (a5/a6/a7) and the Q prologue (a2/a3)
+against the CPU oracle, through the C ABI (flashmap_amd.ops -> ctypes).
+
+Tolerance (written here, from the bar for bf16 outputs): max-abs 2e-2 and mean-abs 2e-3
+against the float32 oracle on the same bf16 inputs. Integer/layout properties
+(paged == contiguous on the same data, fused == unfused prologue) are bit-exact.
+"""
+
+import math
+
+import pytest
+import torch
+
+from _inputs import (check_close, gen, normed_keys, paged_layout, token_pool_from_contig,
+                     vllm_cache_from_contig)
+from oracle import attention as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def ops():
+    from flashmap_amd import ops as o
+
+    return o
+
+
+# ------------------------------------------------------------------- Q prologue
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rms_norm_rope_vllm_table(dev, d):
+    g = gen(1)
+    tokens, heads = 37, 6
+    x = torch.randn(tokens, heads, d, generator=g).bfloat16() * 3
+    w = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(4096, d, 1e6)
+    pos = torch.randint(0, 4096, (tokens,), generator=g)
+    want = ref.rms_norm_rope_vllm(x, w, table, pos, 1e-6)
+    got = ops().rms_norm_rope(x.to(dev), w.to(dev), ops().rope_from_table(table.to(dev)), pos.to(dev), 1e-6)
+    diff = (got.cpu().float() - want.float()).abs()
+    # Bit-exact except where a last-ulp difference of the fp32 mean flips a rounding.
+    exact = (got.cpu() == want).float().mean().item()
+    assert exact > 0.99, f"only {exact:.4f} of elements bit-exact"
+    ulp = want.float().abs() * 2.0 ** -7 + 1e-30
+    assert (diff <= 2 * ulp).all()
+
+
+def test_rms_norm_rope_sglang_freqs(dev):
+    g = gen(2)
+    bs, t, heads, d = 3, 16, 4, 128
+    x = torch.randn(bs, t, heads, d, generator=g).bfloat16()
+    w = torch.ones(d)
+    freqs = ref.rope_freqs(torch.arange(bs * t).view(bs, t) * 7 + 3, d, 1e6)
+    want = ref.rms_norm_rope_sglang(x, w, freqs, 1e-6)
+    got = ops().rms_norm_rope(
+        x.view(-1, heads, d).to(dev), w.to(dev), ops().rope_from_table(freqs.contiguous().to(dev)), None, 1e-6
+    ).view(bs, t, heads, d)
+    assert (got.cpu() == want).float().mean().item() > 0.99
+
+
+# ------------------------------------------------------------ contiguous (a5)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (8, 4), (32, 8), (40, 8)])
+@pytest.mark.parametrize("d", [64, 128])
+def test_contig_attention(dev, hq, hkv, d):
+    g = gen(3)
+    b, t, lmax = 2, 16, 300
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    want = ref.block_attention_contig(q, k, v)
+    got = ops().block_attention_contig(q.to(dev), k.to(dev), v.to(dev))
+    check_close(got, want)
+
+
+def test_contig_attention_seqlens_and_empty(dev):
+    g = gen(4)
+    b, t, hq, hkv, d, lmax = 4, 16, 8, 2, 128, 200
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    lens = torch.tensor([200, 0, 1, 77])
+    want = ref.block_attention_contig(q, k, v, lens)
+    got = ops().block_attention_contig(q.to(dev), k.to(dev), v.to(dev), seqlens_k=lens.to(dev))
+    check_close(got, want)
+    assert (got[1] == 0).all(), "an empty context must give zeros"
+
+
+def test_fused_prologue_is_bit_identical(dev):
+    g = gen(5)
+    b, t, hq, hkv, d, lmax = 3, 16, 32, 8, 128, 160
+    q_pre = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(lmax + t + 1, d, 1e6)
+    pos = (lmax + torch.arange(t))[None].expand(b, -1).reshape(-1)
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    o = ops()
+    rope = o.rope_from_table(table.to(dev))
+    qn = o.rms_norm_rope(q_pre.view(-1, hq, d).to(dev), w.to(dev), rope, pos.to(dev), 1e-6).view(b, t, hq, d)
+    unfused = o.block_attention_contig(qn, k.to(dev), v.to(dev))
+    fused = o.block_attention_contig(
+        q_pre.to(dev), k.to(dev), v.to(dev), prologue=o.Prologue(w.to(dev), rope, pos.to(dev), 1e-6)
+    )
+    assert torch.equal(fused, unfused)
+    want = ref.block_attention_contig(ref.rms_norm_rope_vllm(q_pre.view(-1, hq, d), w, table, pos, 1e-6).view(b, t, hq, d), k, v)
+    check_close(fused, want)
+
+
+# ----------------------------------------------------------------- paged (a6)
+
+
+@pytest.mark.parametrize("hq,hkv,page", [(32, 8, 16), (16, 16, 16), (40, 8, 16), (8, 2, 32), (8, 2, 8)])
+def test_paged_vllm_matches_oracle_and_contig(dev, hq, hkv, page):
+    g = gen(6)
+    d, t = 128, 16
+    lens = torch.tensor([1, 16, 17, 300, 513, 95])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
+    o = ops()
+    got = o.block_attention_paged(
+        q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), t, lmax, d ** -0.5
+    )
+    check_close(got, want)
+    contig = o.block_attention_contig(q.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev), seqlens_k=lens.to(dev))
+    assert torch.equal(got.view(b, t, hq, d), contig), "paged and contiguous layouts must agree bit for bit"
+
+
+def test_paged_zero_length_gives_zeros(dev):
+    g = gen(7)
+    hq, hkv, d, t, page = 8, 2, 128, 16, 16
+    lens = torch.tensor([0, 40, 0])
+    b = len(lens)
+    bt, total = paged_layout(lens, page, g)
+    cache = torch.randn(total, hkv, page, 2 * d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
+    got = ops().block_attention_paged(
+        q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), t, 64, d ** -0.5
+    )
+    check_close(got, want)
+    assert (got[:t] == 0).all() and (got[2 * t:] == 0).all()
+
+
+# ----------------------------------------------------------- token paged (a7)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (32, 8)])
+def test_token_paged_sglang(dev, hq, hkv):
+    g = gen(8)
+    d, t = 128, 16
+    lens = torch.tensor([5, 64, 333, 1])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    kb, vb, pt = token_pool_from_contig(k, v, lens, g)
+    want = ref.block_attention_token_paged(q, kb, vb, lens, pt)
+    got = ops().block_attention_token_paged(q.to(dev), kb.to(dev), vb.to(dev), lens.to(dev, torch.int32), pt.to(dev))
+    check_close(got, want)
+
+
+# ------------------------------------------------------------ self-attention (a8)
+
+
+@pytest.mark.parametrize("heads,d", [(16, 128), (4, 64)])
+def test_block_self_attention(dev, heads, d):
+    g = gen(9)
+    blocks, t = 5, 16
+    qkv = torch.randn(blocks, t, 3, heads, d, generator=g).bfloat16()
+    qn = torch.rand(d, generator=g) + 0.5
+    kn = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(2048, d, 1e6)
+    pos = torch.randint(0, 2000, (blocks * t,), generator=g)
+    rows = table[pos].view(blocks, t, d // 2, 2)
+    want = ref.block_self_attention(qkv, qn, kn, rows[..., 0], rows[..., 1], 1e-6)
+    o = ops()
+    got = o.block_self_attention(qkv.to(dev), qn.to(dev), kn.to(dev), o.rope_from_table(table.to(dev)), pos.to(dev), 1e-6)
+    check_close(got, want)
+
+
+# ---------------------------------------------------------------- writers (a4)
+
+
+def test_write_context_kv_vllm(dev):
+    g = gen(10)
+    tokens, layers, heads, d, page = 9, 3, 4, 128, 16
+    kv = torch.randn(tokens, layers, 2, heads, d, generator=g).bfloat16()
+    kn = torch.rand(layers, d, generator=g) + 0.5
+    table = ref.rope_table(1024, d, 1e6)
+    pos = torch.randint(0, 1000, (tokens,), generator=g)
+    slots = torch.randperm(4 * page, generator=g)[:tokens]
+    slots[3] = -1
+    hpc = 6  # virtual packing: heads of a layer span caches
+    ncache = math.ceil(layers * heads / hpc)
+    caches = [torch.zeros(4, hpc, page, 2 * d, dtype=torch.bfloat16) for _ in range(ncache)]
+    want = [c.clone() for c in caches]
+    ref.write_context_kv_vllm(kv, pos, slots, kn, table, want, page, 1e-6, hpc)
+    o = ops()
+    dcaches = [c.to(dev) for c in caches]
+    ptrs = torch.tensor([c.data_ptr() for c in dcaches], dtype=torch.int64, device=dev)
+    key = dcaches[0][..., :d]
+    strides = (key.stride(0), key.stride(1), key.stride(2), d)
+    o.write_context_kv(kv.to(dev), pos.to(dev), slots.to(dev), kn.to(dev), o.rope_from_table(table.to(dev)),
+                       ptrs, strides, page, 1e-6, hpc)
+    torch.cuda.synchronize()
+    for got, exp in zip(dcaches, want):
+        diff = (got.cpu().float() - exp.float()).abs()
+        assert (got.cpu() == exp).float().mean().item() > 0.99
+        assert diff.max().item() <= 2e-2
+
+
+def test_write_context_kv_pool_sglang(dev):
+    g = gen(11)
+    tokens, layers, heads, d, width = 8, 2, 4, 128, 4
+    kv_size = heads * d
+    kv = torch.randn(tokens, layers * 2 * kv_size, generator=g).bfloat16()
+    kn = torch.rand(layers, d, generator=g) + 0.5
+    cat = ref.rope_cat_table(512, d, 1e6)
+    pos = torch.randint(0, 500, (tokens,), generator=g)
+    locs = torch.randperm(32, generator=g)[:tokens]
+    commit = torch.tensor([3, 1], dtype=torch.int32)
+    kbufs = [torch.zeros(32, heads, d, dtype=torch.bfloat16) for _ in range(layers)]
+    vbufs = [torch.zeros(32, heads, d, dtype=torch.bfloat16) for _ in range(layers)]
+    wk = [x.clone() for x in kbufs]
+    wv = [x.clone() for x in vbufs]
+    ref.write_context_kv_pool(kv, wk, wv, kn, cat, pos, locs, layers, kv_size, d, 1e-6, commit, width)
+    o = ops()
+    dk = [x.to(dev) for x in kbufs]
+    dv = [x.to(dev) for x in vbufs]
+    meta = torch.tensor([[a.data_ptr(), b.data_ptr(), a.stride(0), b.stride(0)] for a, b in zip(dk, dv)],
+                        dtype=torch.int64, device=dev)
+    o.write_context_kv_pool(kv.to(dev), meta, kn.to(dev), o.rope_from_cat(cat.to(dev)), pos.to(dev),
+                            locs.to(dev), layers, kv_size, d, 1e-6, commit.to(dev), width)
+    torch.cuda.synchronize()
+    for got, exp in zip(dk + dv, wk + wv):
+        assert (got.cpu() == exp).float().mean().item() > 0.99
+        assert (got.cpu().float() - exp.float()).abs().max().item() <= 2e-2
