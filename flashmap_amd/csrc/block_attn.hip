@@ -35,9 +35,9 @@
 
 namespace fm {
 
-constexpr int TILE = 32;   // context positions per tile
-constexpr int WAVES = 4;   // wavefronts per workgroup
-constexpr int NRB_MAX = 5; // 16-row blocks per unit
+constexpr int TILE = 32;    // context positions per tile
+constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
+constexpr int STAGES = 4;   // LDS ring depth (tiles)
 
 enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 
@@ -69,25 +69,28 @@ struct AttnArgs {
   float *part_lse;
 };
 
-__device__ __forceinline__ int32_t seq_len(const AttnArgs &a, int b) {
-  if (a.seqlens == nullptr) return a.uniform_len;
-  const int32_t L = a.seqlens[b];
-  return L > 0 ? L : 0;
-}
-__device__ __forceinline__ int64_t tile_prefix(const AttnArgs &a, int b) {
-  return a.plan ? (int64_t)a.plan[b] : (int64_t)b * a.uniform_tiles;
-}
-__device__ __forceinline__ int32_t q_rows_of(const AttnArgs &a, int b) {
-  if (a.cu_q == nullptr) return a.q_len;
-  const int32_t r = a.cu_q[b + 1] - a.cu_q[b];
-  return r < a.q_len ? r : a.q_len;
-}
-// Element offset of query/output row (b, t, head) and the varlen row index of (b, t).
-__device__ __forceinline__ int64_t q_token_index(const AttnArgs &a, int b, int t) {
-  return a.cu_q ? (int64_t)a.cu_q[b] + t : (int64_t)b * a.q_len + t;
-}
+// LDS geometry of one tile stage (bytes). K is stored in MFMA fragment order: block
+// (pb, t) of 1 KB holds, at lane*16, the 8 channels 32t+8g.. of row 16pb+n, i.e. what
+// lane (n, g) feeds to the MFMA. V is stored by rows, RPB rows per 1 KB block, blocks
+// padded by 32 bytes so the transposed 16-bit reads of the P.V operand hit 32 distinct
+// banks.
+template <int D>
+struct Geo {
+  static constexpr int KT = D / 32;            // k-steps over head_dim
+  static constexpr int DB = D / 16;            // 16-channel blocks of O^T
+  static constexpr int KFRAGS = 2 * KT;        // 1 KB K blocks per tile
+  static constexpr int LPR = D / 8;            // 16-byte chunks per row
+  static constexpr int RPB = 64 / LPR;         // V rows per 1 KB block
+  static constexpr int VBLKS = TILE / RPB;     // V blocks per tile
+  static constexpr int VPITCH = 1024 + 32;     // bytes per V block (with pad)
+  static constexpr int NI = KFRAGS + VBLKS;    // 16-byte LDS-DMA loads per lane per tile
+  static constexpr int KBYTES = KFRAGS * 1024;
+  static constexpr int VBYTES = VBLKS * VPITCH;
+  static constexpr int TBYTES = 128;           // page ids of the tile (generic paging)
+  static constexpr int STAGE = KBYTES + VBYTES + TBYTES;
+  static constexpr int SMEM = STAGES * STAGE;
+};
 
-// The share [T0, T1) of workgroup w over `total` tiles, and the workgroup owning tile x.
 __device__ __forceinline__ int64_t share_start(int64_t w, int64_t total, int64_t nw) {
   return w * total / nw;
 }
@@ -95,424 +98,389 @@ __device__ __forceinline__ int64_t share_of(int64_t x, int64_t total, int64_t nw
   return ((x + 1) * nw - 1) / total;
 }
 
-// Offsets (elements) of the context rows of one 16-position half tile: rows
-// p0 .. p0+15 clamped to the last valid position L-1, so padding positions re-read a
-// valid row (their scores are masked) and table lookups stay inside the sequence.
-template <int LAYOUT>
-struct HalfRows {
-  int64_t kbase, vbase;  // PAGED16 / CONTIG: offset of the half's first valid row
-  int32_t lim;           // last valid row index inside the half
+// Read-only per-sequence metadata (uniform loads: scalar when the pointers are noalias).
+struct Meta {
+  const int32_t *__restrict__ plan;
+  const int32_t *__restrict__ seqlens;
+  const int32_t *__restrict__ table;
+  const int32_t *__restrict__ cu_q;
 };
 
-template <int LAYOUT>
-__device__ __forceinline__ HalfRows<LAYOUT> half_rows(const AttnArgs &a, int b, int h, int p0,
-                                                      int L) {
-  HalfRows<LAYOUT> r;
-  const int pe = p0 < L ? p0 : L - 1;
-  r.lim = L - 1 - pe;
-  if (LAYOUT == CONTIG) {
-    r.kbase = (int64_t)b * a.k_s0 + (int64_t)h * a.k_s1 + (int64_t)pe * a.k_s2;
-    r.vbase = (int64_t)b * a.v_s0 + (int64_t)h * a.v_s1 + (int64_t)pe * a.v_s2;
-  } else if (LAYOUT == PAGED16) {
-    int64_t col = pe >> a.page_shift;
-    col = col < a.table_width ? col : a.table_width - 1;
-    int64_t page = a.table[(int64_t)b * a.table_stride + col];
-    page = page < 0 ? 0 : (page >= a.num_pages ? a.num_pages - 1 : page);
-    const int64_t in_page = pe & (a.page_size - 1);
-    r.kbase = page * a.k_s0 + (int64_t)h * a.k_s1 + in_page * a.k_s2;
-    r.vbase = page * a.v_s0 + (int64_t)h * a.v_s1 + in_page * a.v_s2;
-  } else {
-    r.kbase = 0;
-    r.vbase = 0;
-  }
-  return r;
+__device__ __forceinline__ int64_t tile_prefix(const AttnArgs &a, const Meta &m, int b) {
+  return m.plan ? (int64_t)m.plan[b] : (int64_t)b * a.uniform_tiles;
+}
+__device__ __forceinline__ int32_t seq_len(const AttnArgs &a, const Meta &m, int b) {
+  if (m.seqlens == nullptr) return a.uniform_len;
+  const int32_t L = m.seqlens[b];
+  return L > 0 ? L : 0;
+}
+__device__ __forceinline__ int32_t q_rows_of(const AttnArgs &a, const Meta &m, int b) {
+  if (m.cu_q == nullptr) return a.q_len;
+  const int32_t r = m.cu_q[b + 1] - m.cu_q[b];
+  return r < a.q_len ? r : a.q_len;
+}
+__device__ __forceinline__ int64_t q_token_index(const AttnArgs &a, const Meta &m, int b, int t) {
+  return m.cu_q ? (int64_t)m.cu_q[b] + t : (int64_t)b * a.q_len + t;
 }
 
-// Offsets of one context position for the generic paged layout (any page size,
-// including SGLang's page size 1).
-__device__ __forceinline__ void paged_row(const AttnArgs &a, int b, int h, int p, int64_t &ko,
-                                          int64_t &vo) {
-  int64_t col = a.page_size == 1 ? p : p / a.page_size;
+// Position on the workgroup's line of tiles: sequence b, unit ul (= head * rgroups +
+// row group), tile lt of the unit; tiles / L of sequence b.
+struct Cursor {
+  int b, ul, lt, tiles, L;
+};
+
+__device__ __forceinline__ void cursor_load(const AttnArgs &a, const Meta &m, Cursor &c) {
+  c.tiles = (int)(tile_prefix(a, m, c.b + 1) - tile_prefix(a, m, c.b));
+  c.L = seq_len(a, m, c.b);
+}
+
+__device__ __forceinline__ void cursor_next(const AttnArgs &a, const Meta &m, Cursor &c, int ups) {
+  if (++c.lt < c.tiles) return;
+  c.lt = 0;
+  if (++c.ul < ups) return;
+  c.ul = 0;
+  do {
+    ++c.b;
+  } while (c.b < a.batch && tile_prefix(a, m, c.b + 1) == tile_prefix(a, m, c.b));
+  if (c.b < a.batch) cursor_load(a, m, c);
+}
+
+__device__ __forceinline__ Cursor cursor_at(const AttnArgs &a, const Meta &m, int64_t t, int64_t ups) {
+  int lo = 0, hi = a.batch;  // largest b with ups * prefix(b) <= t
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (ups * tile_prefix(a, m, mid) <= t)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  Cursor c;
+  c.b = lo;
+  cursor_load(a, m, c);
+  const int64_t off = t - ups * tile_prefix(a, m, lo);
+  c.ul = (int)(off / c.tiles);
+  c.lt = (int)(off - (int64_t)c.ul * c.tiles);
+  return c;
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+__device__ __forceinline__ void dma16(const void *g, void *l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0): this wavefront's older LDS-DMA loads but the last n
+// are complete, and its LDS reads are done (before a workgroup barrier).
+__device__ __forceinline__ void wait_vm_lgkm0(int n) {
+#define FM_W(N) \
+  case N:       \
+    __builtin_amdgcn_s_waitcnt(((N)&15) | (((N) >> 4) << 14) | (7 << 4)); \
+    break;
+  switch (n) {
+    FM_W(0) FM_W(1) FM_W(2) FM_W(3) FM_W(4) FM_W(5) FM_W(6) FM_W(7) FM_W(8) FM_W(9)
+    FM_W(10) FM_W(11) FM_W(12) FM_W(13) FM_W(14) FM_W(15) FM_W(16) FM_W(17) FM_W(18)
+    FM_W(19) FM_W(20) FM_W(21) FM_W(22) FM_W(23) FM_W(24) FM_W(25) FM_W(26) FM_W(27)
+    FM_W(28) FM_W(29) FM_W(30) FM_W(31) FM_W(32) FM_W(33) FM_W(34) FM_W(35) FM_W(36)
+    FM_W(37) FM_W(38) FM_W(39) FM_W(40) FM_W(41) FM_W(42) FM_W(43) FM_W(44) FM_W(45)
+    FM_W(46) FM_W(47)
+    default:
+      __builtin_amdgcn_s_waitcnt((7 << 4));  // vmcnt(0) lgkmcnt(0)
+  }
+#undef FM_W
+}
+
+__device__ __forceinline__ void block_sync() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Page id of a position for the 16-aligned paged layout (uniform: scalar loads).
+__device__ __forceinline__ int64_t page_of(const AttnArgs &a, const Meta &m, int b, int pos) {
+  int64_t col = pos >> a.page_shift;
   col = col < a.table_width ? col : a.table_width - 1;
-  int64_t page = a.table[(int64_t)b * a.table_stride + col];
-  page = page < 0 ? 0 : (page >= a.num_pages ? a.num_pages - 1 : page);
-  const int64_t in_page = a.page_size == 1 ? 0 : p - col * a.page_size;
-  ko = page * a.k_s0 + (int64_t)h * a.k_s1 + in_page * a.k_s2;
-  vo = page * a.v_s0 + (int64_t)h * a.v_s1 + in_page * a.v_s2;
+  int64_t page = m.table[(int64_t)b * a.table_stride + col];
+  return page < 0 ? 0 : (page >= a.num_pages ? a.num_pages - 1 : page);
 }
 
+// Generic paging: DMA the page ids of the tile's 32 positions (clamped to the
+// sequence) into the stage's table slot. Issued by wavefront 0 only (one instruction).
 template <int D>
-struct TileRegs {
-  u32x4_t kf[2][D / 32];  // K operand: half pb, k-step t: row 16 pb + n, channels 32t+8g..
-  u32x4_t vr[D / 16];     // V rows for the LDS stage: load i covers rows RPL*i + lane/LPR
-};
-
-// Issue the loads of tile `lt` (positions 32*lt ..) of unit (b, h) into `r`.
-template <int LAYOUT, int D>
-__device__ __forceinline__ void issue_tile(const AttnArgs &a, TileRegs<D> &r, int b, int h,
-                                           int lt, int L, int lane) {
-  constexpr int KT = D / 32, VL = D / 16;
-  constexpr int LPR = D / 8;     // lanes per V row (16-byte chunks per row)
-  constexpr int RPL = 64 / LPR;  // V rows per load
-  const int n = lane & 15, g = lane >> 4;
-  const int base = lt * TILE;
-  if (LAYOUT == PAGED) {
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb) {
-      int p = base + 16 * pb + n;
-      p = p < L ? p : L - 1;
-      int64_t ko, vo;
-      paged_row(a, b, h, p, ko, vo);
-      const uint16_t *kp = a.k + ko + 8 * g;
-#pragma unroll
-      for (int t = 0; t < KT; ++t) r.kf[pb][t] = load16(kp + 32 * t);
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      int p = base + RPL * i + lane / LPR;
-      p = p < L ? p : L - 1;
-      int64_t ko, vo;
-      paged_row(a, b, h, p, ko, vo);
-      r.vr[i] = load16(a.v + vo + 8 * (lane % LPR));
-    }
-  } else {
-    HalfRows<LAYOUT> hr[2];
-    hr[0] = half_rows<LAYOUT>(a, b, h, base, L);
-    hr[1] = half_rows<LAYOUT>(a, b, h, base + 16, L);
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb) {
-      const int row = n < hr[pb].lim ? n : hr[pb].lim;
-      const uint16_t *kp = a.k + hr[pb].kbase + (int64_t)row * a.k_s2 + 8 * g;
-#pragma unroll
-      for (int t = 0; t < KT; ++t) r.kf[pb][t] = load16(kp + 32 * t);
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int rv = RPL * i + lane / LPR;  // 0..31
-      const int pb = rv >> 4;
-      int row = rv & 15;
-      row = row < hr[pb].lim ? row : hr[pb].lim;
-      r.vr[i] = load16(a.v + hr[pb].vbase + (int64_t)row * a.v_s2 + 8 * (lane % LPR));
-    }
+__device__ __forceinline__ void issue_table(const AttnArgs &a, const Meta &m, const Cursor &c,
+                                            char *stage, int lane) {
+  using G = Geo<D>;
+  if (lane < 32) {
+    int p = c.lt * TILE + lane;
+    p = p < c.L ? p : c.L - 1;
+    int64_t col = a.page_size == 1 ? p : p / a.page_size;
+    col = col < a.table_width ? col : a.table_width - 1;
+    __builtin_amdgcn_global_load_lds(m.table + (int64_t)c.b * a.table_stride + col,
+                                     (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4, 0, 0);
   }
 }
 
-// Load the unit's query rows into MFMA operand registers (row-quad layout), applying
-// the fused QK-RMSNorm + RoPE when requested. Rows past the unit's valid rows are 0.
-template <int NRB, int D>
-__device__ __forceinline__ void load_queries(const AttnArgs &a, u32x4_t (&qf)[NRB][D / 32], int b,
-                                             int h, int rg, int lane) {
+// This wavefront's share of the K/V LDS-DMA loads of tile c into `stage`:
+// load i = wave, wave + W, ... of the tile's NI loads (K blocks first, then V blocks).
+template <int LAYOUT, int D, int W>
+__device__ __forceinline__ void issue_kv(const AttnArgs &a, const Meta &m, const Cursor &c,
+                                         char *stage, int wave, int lane) {
+  using G = Geo<D>;
+  const int n = lane & 15, g = lane >> 4;
+  const int h = c.ul / a.rgroups;
+  const int pos0 = c.lt * TILE;
+  const int last = c.L - 1 - pos0;  // last valid row of the tile
+  int64_t page0 = 0, page1 = 0;
+  if (LAYOUT == PAGED16) {
+    page0 = page_of(a, m, c.b, pos0);
+    page1 = page_of(a, m, c.b, pos0 + 16 <= c.L - 1 ? pos0 + 16 : c.L - 1);
+  }
+  const int32_t *tbl = reinterpret_cast<const int32_t *>(stage + G::KBYTES + G::VBYTES);
+#pragma unroll
+  for (int k = 0; k < (G::NI + W - 1) / W; ++k) {
+    const int i = wave + k * W;
+    if (i >= G::NI) break;
+    const bool isk = i < G::KFRAGS;
+    int row, coff;
+    char *dst;
+    if (isk) {
+      const int pb = i / G::KT, t = i - (i / G::KT) * G::KT;
+      row = 16 * pb + n;
+      coff = 32 * t + 8 * g;
+      dst = stage + i * 1024;
+    } else {
+      const int vb = i - G::KFRAGS;
+      row = G::RPB * vb + lane / G::LPR;
+      coff = 8 * (lane % G::LPR);
+      dst = stage + G::KBYTES + vb * G::VPITCH;
+    }
+    row = row < last ? row : last;
+    const int64_t s0 = isk ? a.k_s0 : a.v_s0, s1 = isk ? a.k_s1 : a.v_s1, s2 = isk ? a.k_s2 : a.v_s2;
+    const uint16_t *base = isk ? a.k : a.v;
+    int64_t off;
+    if (LAYOUT == CONTIG) {
+      off = (int64_t)c.b * s0 + (int64_t)h * s1 + (int64_t)(pos0 + row) * s2;
+    } else if (LAYOUT == PAGED16) {
+      const int64_t page = row >= 16 ? page1 : page0;
+      off = page * s0 + (int64_t)h * s1 + (int64_t)((pos0 + row) & (a.page_size - 1)) * s2;
+    } else {
+      int64_t page = tbl[row];
+      page = page < 0 ? 0 : (page >= a.num_pages ? a.num_pages - 1 : page);
+      const int p = pos0 + row;
+      const int in_page = a.page_size == 1 ? 0 : p - (p / a.page_size) * a.page_size;
+      off = page * s0 + (int64_t)h * s1 + (int64_t)in_page * s2;
+    }
+    dma16(base + off + coff, dst);
+  }
+}
+
+// Query rows of this wavefront (row block `wave` of unit (b, h, rg)) as the MFMA B
+// operand, with the fused QK-RMSNorm + RoPE when requested. Invalid rows are 0.
+template <int D, int W>
+__device__ __forceinline__ void load_queries(const AttnArgs &a, const Meta &m, u32x4_t (&qf)[D / 32],
+                                             int b, int h, int rg, int wave, int lane) {
   constexpr int KT = D / 32;
   const int n = lane & 15, g = lane >> 4;
-  const int qlen_b = q_rows_of(a, b);
+  const int R = (rg * W + wave) * 16 + n;
+  const int gq = R / a.q_len, tq = R - gq * a.q_len;
+  const bool valid = gq < a.group && tq < q_rows_of(a, m, b);
+  const int64_t tok = q_token_index(a, m, b, valid ? tq : 0);
+  const int64_t head = (int64_t)h * a.group + (valid ? gq : 0);
+  const uint16_t *src = a.q + (m.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)tq * a.q_st) +
+                        head * a.q_sh + 8 * g;
 #pragma unroll
-  for (int rb = 0; rb < NRB; ++rb) {
-    const int R = (rg * NRB + rb) * 16 + n;
-    const int gq = R / a.q_len, tq = R - gq * a.q_len;
-    const bool valid = gq < a.group && tq < qlen_b;
-    const int64_t tok = q_token_index(a, b, valid ? tq : 0);
-    const int64_t head = (int64_t)h * a.group + (valid ? gq : 0);
-    const uint16_t *src =
-        a.q + (a.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)tq * a.q_st) + head * a.q_sh +
-        8 * g;
-#pragma unroll
-    for (int t = 0; t < KT; ++t) qf[rb][t] = valid ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
-    if (a.qn_w != nullptr) {
-      const int64_t rr = clamp_row(a.rope, valid ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
-      norm_rope_row<D>(qf[rb], a.qn_w, a.eps, a.rope, rr, g);
-    }
+  for (int t = 0; t < KT; ++t) qf[t] = valid ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
+  if (a.qn_w != nullptr) {
+    const int64_t rr = clamp_row(a.rope, valid ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
+    norm_rope_row<D>(qf, a.qn_w, a.eps, a.rope, rr, g);
   }
 }
 
-template <int NRB, int D>
-struct WaveState {
-  f32x4_t acc[NRB][D / 16];  // O^T[d = 16 db + 4 g + i][row = 16 rb + n]
-  float m[NRB];              // running max (log2 domain), uniform over lane groups
-  float l[NRB];              // running sum, lane-partial (this lane's positions)
-};
-
-// One tile: stage V in LDS, S^T = K Q^T, online softmax, O^T += V^T P^T.
-template <int NRB, int D>
-__device__ __forceinline__ void compute_tile(const AttnArgs &a, const TileRegs<D> &r,
-                                             const u32x4_t (&qf)[NRB][D / 32],
-                                             WaveState<NRB, D> &st, uint16_t *vs, int tile_base,
-                                             int L, int lane) {
-  constexpr int KT = D / 32, DB = D / 16, VL = D / 16;
-  constexpr int LPR = D / 8, RPL = 64 / LPR;
-  constexpr int VP = D + 4;  // LDS row pitch (elements): conflict-free transposed reads
+// One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T.
+template <int D>
+__device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stage,
+                                             const u32x4_t (&qf)[D / 32], f32x4_t (&acc)[D / 16],
+                                             float &m, float &l, int pos0, int L, int lane) {
+  using G = Geo<D>;
   const int n = lane & 15, g = lane >> 4;
-
-  // V rows into this wavefront's LDS stage.
-#pragma unroll
-  for (int i = 0; i < VL; ++i) {
-    const int rv = RPL * i + lane / LPR;
-    uint16_t *dst = vs + rv * VP + 8 * (lane % LPR);
-    *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{r.vr[i][0], r.vr[i][1]};
-    *reinterpret_cast<u32x2_t *>(dst + 4) = u32x2_t{r.vr[i][2], r.vr[i][3]};
-  }
-
-  // S^T = K Q^T for both halves and every row block.
-  f32x4_t s[2][NRB];
+  f32x4_t s[2];
 #pragma unroll
   for (int pb = 0; pb < 2; ++pb) {
+    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < KT; ++t) c = mfma_16x16x32(r.kf[pb][t], qf[rb][t], c);
-      s[pb][rb] = c;
+    for (int t = 0; t < G::KT; ++t) {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(stage + (pb * G::KT + t) * 1024 + lane * 16);
+      c = mfma_16x16x32(kf, qf[t], c);
     }
+    s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
   }
-  if (tile_base + TILE > L) {
+  if (pos0 + TILE > L) {
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (tile_base + 16 * pb + 4 * g + i >= L)
-#pragma unroll
-          for (int rb = 0; rb < NRB; ++rb) s[pb][rb][i] = -INFINITY;
+        if (pos0 + 16 * pb + 4 * g + i >= L) s[pb][i] = -INFINITY;
   }
-
-  // Online softmax (log2 domain) and P^T as the bf16 B operand.
-  u32x4_t pk[NRB];
+  float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                   fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+  mx = max_over_groups(mx);
+  const float mnew = fmaxf(m, mx * a.scale_log2);
+  const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+  m = mnew;
+  float p[2][4];
+  float ps = 0.f;
 #pragma unroll
-  for (int rb = 0; rb < NRB; ++rb) {
-    float mx = s[0][rb][0];
+  for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+    for (int i = 0; i < 4; ++i) {
+      p[pb][i] = __builtin_amdgcn_exp2f(fmaf(s[pb][i], a.scale_log2, -mnew));
+      ps += p[pb][i];
+    }
+  l = l * alpha + ps;
+  const u32x4_t pk = {pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                      pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+  // V^T operand: row d = 16 db + n, reduction positions pos(g, j) = 4g + j (j < 4) and
+  // 16 + 4g + j - 4 (j >= 4), the positions of this lane's S^T values.
+  const uint16_t *vs = reinterpret_cast<const uint16_t *>(stage + G::KBYTES);
+  int vo[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[pb][rb][i]);
-    mx = max_over_groups(mx);
-    const float mnew = fmaxf(st.m[rb], mx * a.scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f(st.m[rb] - mnew);
-    st.m[rb] = mnew;
-    float p[2][4];
-    float ps = 0.f;
-#pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[pb][i] = __builtin_amdgcn_exp2f(fmaf(s[pb][rb][i], a.scale_log2, -mnew));
-        ps += p[pb][i];
-      }
-    st.l[rb] = st.l[rb] * alpha + ps;
-    pk[rb] = u32x4_t{pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
-                     pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
-#pragma unroll
-    for (int db = 0; db < DB; ++db) st.acc[rb][db] *= alpha;
+  for (int j = 0; j < 8; ++j) {
+    const int pos = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+    vo[j] = (pos / G::RPB) * (G::VPITCH / 2) + (pos % G::RPB) * D + n;
   }
-
-  __builtin_amdgcn_wave_barrier();
-  // O^T += V^T P^T: A operand row d = 16 db + n, reduction positions
-  // {4g, 4g+1, 4g+2, 4g+3, 16+4g, .., 16+4g+3} (the S^T accumulator positions).
-  const uint16_t *vcol = vs + 4 * g * VP + n;
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    const uint16_t *c0 = vcol + 16 * db;
+  for (int db = 0; db < G::DB; ++db) {
+    const uint16_t *c0 = vs + 16 * db;
     u32x4_t vf;
-    vf[0] = (uint32_t)c0[0 * VP] | ((uint32_t)c0[1 * VP] << 16);
-    vf[1] = (uint32_t)c0[2 * VP] | ((uint32_t)c0[3 * VP] << 16);
-    vf[2] = (uint32_t)c0[16 * VP] | ((uint32_t)c0[17 * VP] << 16);
-    vf[3] = (uint32_t)c0[18 * VP] | ((uint32_t)c0[19 * VP] << 16);
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) st.acc[rb][db] = mfma_16x16x32(vf, pk[rb], st.acc[rb][db]);
+    vf[0] = (uint32_t)c0[vo[0]] | ((uint32_t)c0[vo[1]] << 16);
+    vf[1] = (uint32_t)c0[vo[2]] | ((uint32_t)c0[vo[3]] << 16);
+    vf[2] = (uint32_t)c0[vo[4]] | ((uint32_t)c0[vo[5]] << 16);
+    vf[3] = (uint32_t)c0[vo[6]] | ((uint32_t)c0[vo[7]] << 16);
+    acc[db] = mfma_16x16x32(vf, pk, acc[db] * alpha);
   }
-  __builtin_amdgcn_wave_barrier();
 }
 
-template <int NRB, int D>
-constexpr int smem_bytes() {
-  constexpr int stage = WAVES * TILE * (D + 4) * 2;
-  constexpr int combine = 2 * NRB * (D / 16) * 64 * 16 + 2 * WAVES * NRB * 16 * 4;
-  return stage > combine ? stage : combine;
-}
-
-template <int LAYOUT, int NRB, int D>
-__global__ __launch_bounds__(256, 1) void attn_fwd_kernel(const AttnArgs a) {
-  constexpr int DB = D / 16;
-  constexpr int ROWS = NRB * 16;
-  __shared__ __attribute__((aligned(16))) char smem[smem_bytes<NRB, D>()];
+template <int LAYOUT, int W, int D>
+__global__ __launch_bounds__(64 * W) void attn_fwd_kernel(
+    const AttnArgs a, const int32_t *__restrict__ plan, const int32_t *__restrict__ seqlens,
+    const int32_t *__restrict__ table, const int32_t *__restrict__ cu_q) {
+  using G = Geo<D>;
+  __shared__ __attribute__((aligned(1024))) char smem[G::SMEM];
+  const Meta mt{plan, seqlens, table, cu_q};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-
-  const int64_t ups = (int64_t)a.hkv * a.rgroups;
-  const int64_t total = ups * tile_prefix(a, a.batch);
-  const int64_t nw = a.num_wg;
-  const int64_t T0 = share_start(blockIdx.x, total, nw);
-  const int64_t T1 = share_start((int64_t)blockIdx.x + 1, total, nw);
+  const int ups = a.hkv * a.rgroups;
+  const int64_t total = (int64_t)ups * tile_prefix(a, mt, a.batch);
+  const int64_t T0 = share_start(blockIdx.x, total, a.num_wg);
+  const int64_t T1 = share_start((int64_t)blockIdx.x + 1, total, a.num_wg);
   if (T0 >= T1) return;
+  const int ntiles = (int)(T1 - T0);
+  // Loads this wavefront issues per tile, and per tile for wavefront 0's page ids.
+  const int ipw = (G::NI - wave + W - 1) / W;
+  constexpr bool TBL = LAYOUT == PAGED;
 
-  // Sequence of the first tile: the largest b with ups * prefix(b) <= T0.
-  int b = 0;
-  {
-    int lo = 0, hi = a.batch;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (ups * tile_prefix(a, mid) <= T0)
-        lo = mid;
-      else
-        hi = mid;
+  Cursor cc = cursor_at(a, mt, T0, ups);  // tile being computed (i)
+  Cursor ci = cc;                         // tile being loaded (i + STAGES - 1)
+  Cursor ct = cc;                         // tile whose page ids are loaded (i + STAGES)
+  if (TBL) {
+    for (int j = 0; j < STAGES && j < ntiles; ++j) {
+      if (wave == 0) issue_table<D>(a, mt, ct, smem + j * G::STAGE, lane);
+      if (j + 1 < ntiles) cursor_next(a, mt, ct, ups);
     }
-    b = lo;
+    wait_vm_lgkm0(0);
+    block_sync();
+  }
+  for (int j = 0; j < STAGES - 1 && j < ntiles; ++j) {
+    issue_kv<LAYOUT, D, W>(a, mt, ci, smem + j * G::STAGE, wave, lane);
+    if (j + 1 < ntiles) cursor_next(a, mt, ci, ups);
   }
 
-  uint16_t *vstage = reinterpret_cast<uint16_t *>(smem) + wave * TILE * (D + 4);
-  float *obuf = reinterpret_cast<float *>(smem);                       // [2][NRB][DB][64][4]
-  float *m_s = obuf + 2 * NRB * DB * 64 * 4;                           // [WAVES][ROWS]
-  float *l_s = m_s + WAVES * ROWS;                                      // [WAVES][ROWS]
-
-  int64_t t = T0;
-  int seg = 0;
-  while (t < T1) {
-    while (b + 1 < a.batch && ups * tile_prefix(a, b + 1) <= t) ++b;
-    const int64_t sb = ups * tile_prefix(a, b);
-    const int tiles_b = (int)(tile_prefix(a, b + 1) - tile_prefix(a, b));
-    const int64_t off = t - sb;
-    const int ul = (int)(off / tiles_b);
-    const int lt0 = (int)(off - (int64_t)ul * tiles_b);
-    const int64_t rem = T1 - t;
-    const int lt1 = (int64_t)(tiles_b - lt0) < rem ? tiles_b : lt0 + (int)rem;
-    const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
-    const int L = seq_len(a, b);
-
-    u32x4_t qf[NRB][D / 32];
-    load_queries<NRB, D>(a, qf, b, h, rg, lane);
-
-    WaveState<NRB, D> st;
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-      st.m[rb] = -INFINITY;
-      st.l[rb] = 0.f;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) st.acc[rb][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-
-    // This wavefront's tiles: lt0 + wave, + WAVES, ... (register double buffer).
-    TileRegs<D> buf0, buf1;
-    int lt = lt0 + wave;
-    if (lt < lt1) issue_tile<LAYOUT, D>(a, buf0, b, h, lt, L, lane);
-    while (lt < lt1) {
-      int ltn = lt + WAVES;
-      if (ltn < lt1) issue_tile<LAYOUT, D>(a, buf1, b, h, ltn, L, lane);
-      compute_tile<NRB, D>(a, buf0, qf, st, vstage, lt * TILE, L, lane);
-      lt = ltn;
-      if (lt >= lt1) break;
-      ltn = lt + WAVES;
-      if (ltn < lt1) issue_tile<LAYOUT, D>(a, buf0, b, h, ltn, L, lane);
-      compute_tile<NRB, D>(a, buf1, qf, st, vstage, lt * TILE, L, lane);
-      lt = ltn;
-    }
-
-    // Merge the four wavefronts: common max, rescale, tree-sum of O^T in LDS.
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) st.l[rb] = sum_over_groups(st.l[rb]);
-    __syncthreads();  // every wavefront is done with its V stage (aliased below)
-    if (g == 0) {
-#pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) {
-        m_s[wave * ROWS + rb * 16 + n] = st.m[rb];
-        l_s[wave * ROWS + rb * 16 + n] = st.l[rb];
+  u32x4_t qf[D / 32];
+  f32x4_t acc[D / 16];
+  float m = -INFINITY, l = 0.f;
+  int seg = 0, lt_first = 0;
+  for (int i = 0; i < ntiles; ++i) {
+    // Tile i is complete once every later load of this wavefront is allowed to be
+    // outstanding: the K/V loads of tiles i+1 .. i+STAGES-2 (and, on wavefront 0,
+    // the page-id loads issued after tile i's).
+    {
+      const int later = min(STAGES - 2, ntiles - 1 - i);
+      int nwait = ipw * (later > 0 ? later : 0);
+      if (TBL && wave == 0) {
+        const int lo = max(i + 2, STAGES), hi = min(i + STAGES - 1, ntiles - 1);
+        nwait += hi >= lo ? hi - lo + 1 : 0;
+        // page ids of tile i + STAGES - 1 (issued last iteration, before its K/V loads)
+        if (i >= 1 && i + STAGES - 1 < ntiles) nwait = min(nwait, i + STAGES - 2 < ntiles ? ipw : 0);
       }
+      wait_vm_lgkm0(nwait);
     }
-    __syncthreads();
-    float inv_l[NRB], lse[NRB];
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb) {
-      const int row = rb * 16 + n;
-      float M = m_s[row];
-#pragma unroll
-      for (int w = 1; w < WAVES; ++w) M = fmaxf(M, m_s[w * ROWS + row]);
-      float Lt = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const float mw = m_s[w * ROWS + row];
-        Lt += mw == -INFINITY ? 0.f : l_s[w * ROWS + row] * __builtin_amdgcn_exp2f(mw - M);
-      }
-      const float f = st.m[rb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.m[rb] - M);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) st.acc[rb][db] *= f;
-      inv_l[rb] = Lt > 0.f ? 1.f / Lt : 0.f;
-      lse[rb] = M + log2f(Lt);
+    block_sync();
+    if (TBL && i + STAGES < ntiles) {
+      if (wave == 0) issue_table<D>(a, mt, ct, smem + ((i + STAGES) % STAGES) * G::STAGE, lane);
+      cursor_next(a, mt, ct, ups);
     }
-    f32x4_t *ob = reinterpret_cast<f32x4_t *>(obuf);
-    if (wave >= 2) {
-#pragma unroll
-      for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) ob[(((wave - 2) * NRB + rb) * DB + db) * 64 + lane] = st.acc[rb][db];
+    if (i + STAGES - 1 < ntiles) {
+      issue_kv<LAYOUT, D, W>(a, mt, ci, smem + ((i + STAGES - 1) % STAGES) * G::STAGE, wave, lane);
+      if (i + STAGES < ntiles) cursor_next(a, mt, ci, ups);
     }
-    __syncthreads();
-    if (wave < 2) {
-#pragma unroll
-      for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) st.acc[rb][db] += ob[((wave * NRB + rb) * DB + db) * 64 + lane];
-    }
-    __syncthreads();
-    if (wave == 1) {
-#pragma unroll
-      for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) ob[(rb * DB + db) * 64 + lane] = st.acc[rb][db];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) st.acc[rb][db] += ob[(rb * DB + db) * 64 + lane];
-    }
-    __syncthreads();  // LDS is free for the next segment's V stage
 
-    if (wave == 0) {
-      const bool whole = lt0 == 0 && lt1 == tiles_b;
-      const int qlen_b = q_rows_of(a, b);
-      const int64_t slot = 2 * (int64_t)blockIdx.x + (seg == 0 ? 0 : 1);
+    const int h = cc.ul / a.rgroups, rg = cc.ul - h * a.rgroups;
+    if (i == 0 || cc.lt == 0) {  // a unit (segment) starts
+      load_queries<D, W>(a, mt, qf, cc.b, h, rg, wave, lane);
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) {
-        const int R = (rg * NRB + rb) * 16 + n;
-        const int gq = R / a.q_len, tq = R - gq * a.q_len;
-        if (gq >= a.group || tq >= qlen_b) continue;
+      for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      m = -INFINITY;
+      l = 0.f;
+      lt_first = cc.lt;
+    }
+    compute_tile<D>(a, smem + (i % STAGES) * G::STAGE, qf, acc, m, l, cc.lt * TILE, cc.L, lane);
+
+    if (cc.lt == cc.tiles - 1 || i == ntiles - 1) {  // the segment ends: write it out
+      const float lt_sum = sum_over_groups(l);
+      const float inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
+      const bool whole = lt_first == 0 && cc.lt == cc.tiles - 1;
+      const int R = (rg * W + wave) * 16 + n;
+      const int gq = R / a.q_len, tq = R - gq * a.q_len;
+      if (gq < a.group && tq < q_rows_of(a, mt, cc.b)) {
         if (whole) {
           const int64_t head = (int64_t)h * a.group + gq;
           uint16_t *dst = a.o +
-                          (a.cu_q ? q_token_index(a, b, tq) * a.o_st
-                                  : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
+                          (cu_q ? q_token_index(a, mt, cc.b, tq) * a.o_st
+                                : (int64_t)cc.b * a.o_sb + (int64_t)tq * a.o_st) +
                           head * a.o_sh + 4 * g;
 #pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const f32x4_t v = st.acc[rb][db] * inv_l[rb];
+          for (int db = 0; db < D / 16; ++db) {
+            const f32x4_t v = acc[db] * inv;
             *reinterpret_cast<u32x2_t *>(dst + 16 * db) =
                 u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           }
         } else {
-          const int64_t prow = slot * ROWS + rb * 16 + n;
+          const int64_t slot = 2 * (int64_t)blockIdx.x + (seg == 0 ? 0 : 1);
+          const int64_t prow = slot * (16 * W) + wave * 16 + n;
           float *dst = a.part_o + prow * D + 4 * g;
 #pragma unroll
-          for (int db = 0; db < DB; ++db)
-            *reinterpret_cast<f32x4_t *>(dst + 16 * db) = st.acc[rb][db] * inv_l[rb];
-          if (g == 0) a.part_lse[prow] = lse[rb];
+          for (int db = 0; db < D / 16; ++db) *reinterpret_cast<f32x4_t *>(dst + 16 * db) = acc[db] * inv;
+          if (g == 0) a.part_lse[prow] = m + log2f(lt_sum);
         }
       }
+      ++seg;
     }
-    t += lt1 - lt0;
-    ++seg;
+    if (i + 1 < ntiles) cursor_next(a, mt, cc, ups);
   }
 }
 
 // Merge the partials of units cut between workgroups; zero-fill empty sequences.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, int nrb) {
+  const Meta mt{a.plan, a.seqlens, a.table, a.cu_q};
   const int rows = nrb * 16;
   const int64_t ups = (int64_t)a.hkv * a.rgroups;
   const int64_t unit = blockIdx.x;
   const int b = (int)(unit / ups);
   const int ul = (int)(unit - (int64_t)b * ups);
   const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
-  const int64_t pre = tile_prefix(a, b);
-  const int tiles_b = (int)(tile_prefix(a, b + 1) - pre);
-  const int qlen_b = q_rows_of(a, b);
-  const int64_t total = ups * tile_prefix(a, a.batch);
+  const int64_t pre = tile_prefix(a, mt, b);
+  const int tiles_b = (int)(tile_prefix(a, mt, b + 1) - pre);
+  const int qlen_b = q_rows_of(a, mt, b);
+  const int64_t total = ups * tile_prefix(a, mt, a.batch);
   const int64_t nw = a.num_wg;
   int64_t wa = 0, wb = 0, U0 = 0;
   if (tiles_b > 0) {
@@ -548,7 +516,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, int
     }
     const int64_t head = (int64_t)h * a.group + gq;
     uint16_t *dst = a.o +
-                    (a.cu_q ? q_token_index(a, b, tq) * a.o_st
+                    (a.cu_q ? q_token_index(a, mt, b, tq) * a.o_st
                             : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
                     head * a.o_sh + 4 * c;
     *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
@@ -582,28 +550,32 @@ __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restri
 // ---------------------------------------------------------------------------------
 // Host side: grid sizing, workspace layout, dispatch.
 
-typedef void (*AttnKernel)(const AttnArgs);
+typedef void (*AttnKernel)(const AttnArgs, const int32_t *, const int32_t *, const int32_t *,
+                           const int32_t *);
 
 template <int LAYOUT, int D>
-static AttnKernel pick_kernel(int nrb) {
-  switch (nrb) {
+static AttnKernel pick_kernel(int w) {
+  switch (w) {
     case 1: return attn_fwd_kernel<LAYOUT, 1, D>;
     case 2: return attn_fwd_kernel<LAYOUT, 2, D>;
     case 3: return attn_fwd_kernel<LAYOUT, 3, D>;
     case 4: return attn_fwd_kernel<LAYOUT, 4, D>;
-    default: return attn_fwd_kernel<LAYOUT, 5, D>;
+    case 5: return attn_fwd_kernel<LAYOUT, 5, D>;
+    case 6: return attn_fwd_kernel<LAYOUT, 6, D>;
+    case 7: return attn_fwd_kernel<LAYOUT, 7, D>;
+    default: return attn_fwd_kernel<LAYOUT, 8, D>;
   }
 }
 
-static AttnKernel select_kernel(int layout, int d, int nrb) {
+static AttnKernel select_kernel(int layout, int d, int w) {
   if (d == 128) {
-    if (layout == CONTIG) return pick_kernel<CONTIG, 128>(nrb);
-    if (layout == PAGED16) return pick_kernel<PAGED16, 128>(nrb);
-    return pick_kernel<PAGED, 128>(nrb);
+    if (layout == CONTIG) return pick_kernel<CONTIG, 128>(w);
+    if (layout == PAGED16) return pick_kernel<PAGED16, 128>(w);
+    return pick_kernel<PAGED, 128>(w);
   }
-  if (layout == CONTIG) return pick_kernel<CONTIG, 64>(nrb);
-  if (layout == PAGED16) return pick_kernel<PAGED16, 64>(nrb);
-  return pick_kernel<PAGED, 64>(nrb);
+  if (layout == CONTIG) return pick_kernel<CONTIG, 64>(w);
+  if (layout == PAGED16) return pick_kernel<PAGED16, 64>(w);
+  return pick_kernel<PAGED, 64>(w);
 }
 
 struct RowPlan {
@@ -611,16 +583,12 @@ struct RowPlan {
   int rgroups;  // units per KV head
 };
 
+// Row blocks per unit (= wavefronts per workgroup) and row groups per KV head.
 static RowPlan row_plan(int group, int q_len) {
   const int total = (group * q_len + 15) / 16;
   RowPlan p;
-  if (total <= NRB_MAX) {
-    p.rgroups = 1;
-    p.nrb = total;
-  } else {
-    p.rgroups = (total + 3) / 4;
-    p.nrb = (total + p.rgroups - 1) / p.rgroups;
-  }
+  p.rgroups = (total + NRB_MAX - 1) / NRB_MAX;
+  p.nrb = (total + p.rgroups - 1) / p.rgroups;
   return p;
 }
 
@@ -631,14 +599,14 @@ static int env_int(const char *name, int dflt) {
 }
 
 // Workgroups resident per CU for a kernel (cached).
-static int occupancy(AttnKernel k) {
+static int occupancy(AttnKernel k, int block) {
   static std::mutex mu;
   static std::vector<std::pair<AttnKernel, int>> cache;
   std::lock_guard<std::mutex> lock(mu);
   for (auto &e : cache)
     if (e.first == k) return e.second;
   int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void *>(k), 256,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void *>(k), block,
                                                    0) != hipSuccess ||
       blocks < 1)
     blocks = 1;
@@ -664,7 +632,7 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + TILE - 1) / TILE);
   const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
-  int64_t nw = (int64_t)info.cus * occupancy(k);
+  int64_t nw = (int64_t)info.cus * occupancy(k, 64 * sz->rp.nrb);
   const int cap = env_int("FLASHMAP_SPLITKV_WORKGROUPS", 0);
   if (cap > 0) nw = cap;
   const int64_t want = (tiles_bound + min_tiles - 1) / min_tiles;
@@ -758,10 +726,11 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
     a.uniform_tiles = (a.uniform_len + TILE - 1) / TILE;
   }
   AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb);
-  void *kargs[] = {&a};
+  const int32_t *kplan = a.plan, *kseq = a.seqlens, *ktab = a.table, *kcu = a.cu_q;
+  void *kargs[] = {&a, &kplan, &kseq, &ktab, &kcu};
   profile_before(c.stream);
-  const hipError_t lerr = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(sz.num_wg), dim3(256),
-                                          kargs, 0, c.stream);
+  const hipError_t lerr = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(sz.num_wg),
+                                          dim3(64 * sz.rp.nrb), kargs, 0, c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
   const int64_t units = (int64_t)c.batch * c.hkv * sz.rp.rgroups;
