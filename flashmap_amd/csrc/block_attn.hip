@@ -15,17 +15,19 @@
 // flashmap/sglang/verify_attention.py:184-233). Only the first and last segment of a
 // share can be cut, so two partial slots per workgroup suffice.
 //
-// Per tile and wavefront (16-row blocks rb, 16-position halves pb):
-//   S^T[pos][row] = K Q^T     (v_mfma_f32_16x16x32_bf16, A = K rows straight from HBM,
-//                              B = Q rows in registers)
-//   online softmax on S^T: each lane owns one row (lane % 16), so the running max,
-//   sum and rescale are lane-local; only the max crosses the 4 lane groups.
-//   O^T[d][row] += V^T P^T    (B = P^T is exactly the S^T accumulator layout rounded
-//                              to bf16; A = V^T is read transposed out of LDS, where
-//                              the V tile was staged with 16-byte loads)
-// K is read from HBM with 16-byte loads in MFMA operand layout (64 contiguous bytes
-// per row per instruction); V with fully contiguous 16-byte loads. The next tile's K
-// and V are loaded while the current one is computed (register double buffer).
+// Workgroup = one wavefront per 16-row block of the unit (4 at GQA 4 x 16 rows). All
+// wavefronts walk the share's tiles together: K/V tiles stream from HBM straight into
+// an LDS ring of STAGES tiles with LDS-DMA (global_load_lds_dwordx4, no registers in
+// flight), each wavefront issuing an equal part of every tile's 16-byte loads; tile i
+// is consumed after a hand-counted s_waitcnt vmcnt and a barrier while tiles
+// i+1 .. i+STAGES-1 are in flight. K lands in LDS already in MFMA operand order.
+// Per tile, wavefront w (its 16 rows r):
+//   S^T[pos][r] = K Q^T       v_mfma_f32_16x16x32_bf16, A = K from LDS, B = Q in registers
+//   online softmax on S^T:    each lane owns one row (lane % 16): the running max, sum
+//                             and rescale are lane-local; the max crosses 4 lane groups
+//   O^T[d][r] += V^T P^T      B = P^T is the S^T accumulator rounded to bf16 as is;
+//                             A = V^T is read transposed out of LDS (16-bit reads)
+// so no wavefront exchanges data with another and each writes its own rows.
 #include <math.h>
 
 #include <mutex>
@@ -57,6 +59,7 @@ struct AttnArgs {
   int32_t page_size, page_shift;
   const int32_t *seqlens;  // NULL: every sequence has uniform_len positions
   int32_t uniform_len, uniform_tiles;
+  int32_t pos_cap;  // CONTIG: positions the K/V tensors hold (reads are clamped below it)
   int32_t batch, hkv, group, rgroups;
   float scale_log2;
   const float *qn_w;  // non-NULL: fused Q prologue
@@ -106,21 +109,35 @@ struct Meta {
   const int32_t *__restrict__ cu_q;
 };
 
+// Scalar (SMEM) load of a wave-uniform int32 that no kernel of this call writes
+// (plans, lengths, tables). Completion is awaited inside, on lgkmcnt, so it never
+// joins the vmcnt-ordered stream of LDS-DMA loads whose waits are counted by hand.
+__device__ __forceinline__ int32_t sload(const int32_t *p) {
+  int32_t v;
+  // Both halves of the address are zero-extended (readfirstlane returns a signed int).
+  const uint64_t addr = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));
+  const int32_t *u = reinterpret_cast<const int32_t *>(((uint64_t)hi << 32) | (uint64_t)lo);
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(u));
+  return v;
+}
+
 __device__ __forceinline__ int64_t tile_prefix(const AttnArgs &a, const Meta &m, int b) {
-  return m.plan ? (int64_t)m.plan[b] : (int64_t)b * a.uniform_tiles;
+  return m.plan ? (int64_t)sload(m.plan + b) : (int64_t)b * a.uniform_tiles;
 }
 __device__ __forceinline__ int32_t seq_len(const AttnArgs &a, const Meta &m, int b) {
   if (m.seqlens == nullptr) return a.uniform_len;
-  const int32_t L = m.seqlens[b];
+  const int32_t L = sload(m.seqlens + b);
   return L > 0 ? L : 0;
 }
 __device__ __forceinline__ int32_t q_rows_of(const AttnArgs &a, const Meta &m, int b) {
   if (m.cu_q == nullptr) return a.q_len;
-  const int32_t r = m.cu_q[b + 1] - m.cu_q[b];
+  const int32_t r = sload(m.cu_q + b + 1) - sload(m.cu_q + b);
   return r < a.q_len ? r : a.q_len;
 }
 __device__ __forceinline__ int64_t q_token_index(const AttnArgs &a, const Meta &m, int b, int t) {
-  return m.cu_q ? (int64_t)m.cu_q[b] + t : (int64_t)b * a.q_len + t;
+  return m.cu_q ? (int64_t)sload(m.cu_q + b) + t : (int64_t)b * a.q_len + t;
 }
 
 // Position on the workgroup's line of tiles: sequence b, unit ul (= head * rgroups +
@@ -198,7 +215,7 @@ __device__ __forceinline__ void block_sync() {
 __device__ __forceinline__ int64_t page_of(const AttnArgs &a, const Meta &m, int b, int pos) {
   int64_t col = pos >> a.page_shift;
   col = col < a.table_width ? col : a.table_width - 1;
-  int64_t page = m.table[(int64_t)b * a.table_stride + col];
+  int64_t page = sload(m.table + (int64_t)b * a.table_stride + col);
   return page < 0 ? 0 : (page >= a.num_pages ? a.num_pages - 1 : page);
 }
 
@@ -227,7 +244,8 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Meta &m, const
   const int n = lane & 15, g = lane >> 4;
   const int h = c.ul / a.rgroups;
   const int pos0 = c.lt * TILE;
-  const int last = c.L - 1 - pos0;  // last valid row of the tile
+  int last = c.L - 1 - pos0;  // last valid row of the tile
+  last = last > 0 ? last : 0;  // (never negative, even for a plan that disagrees with L)
   int64_t page0 = 0, page1 = 0;
   if (LAYOUT == PAGED16) {
     page0 = page_of(a, m, c.b, pos0);
@@ -257,7 +275,8 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Meta &m, const
     const uint16_t *base = isk ? a.k : a.v;
     int64_t off;
     if (LAYOUT == CONTIG) {
-      off = (int64_t)c.b * s0 + (int64_t)h * s1 + (int64_t)(pos0 + row) * s2;
+      const int p = pos0 + row < a.pos_cap ? pos0 + row : a.pos_cap - 1;
+      off = (int64_t)c.b * s0 + (int64_t)h * s1 + (int64_t)p * s2;
     } else if (LAYOUT == PAGED16) {
       const int64_t page = row >= 16 ? page1 : page0;
       off = page * s0 + (int64_t)h * s1 + (int64_t)((pos0 + row) & (a.page_size - 1)) * s2;
@@ -292,6 +311,11 @@ __device__ __forceinline__ void load_queries(const AttnArgs &a, const Meta &m, u
     const int64_t rr = clamp_row(a.rope, valid ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
     norm_rope_row<D>(qf, a.qn_w, a.eps, a.rope, rr, g);
   }
+  // Settle the query registers here, at the segment start: their loads are then no
+  // longer pending anywhere in the tile loop, so the compiler does not drain the
+  // LDS-DMA pipeline (vmcnt(0)) before each tile's first MFMA.
+#pragma unroll
+  for (int t = 0; t < KT; ++t) asm volatile("" : "+v"(qf[t]));
 }
 
 // One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T.
@@ -818,8 +842,10 @@ extern "C" int fm_block_attn_contig(
   a.v = (const uint16_t *)v;
   a.k_s0 = k_stride_batch, a.k_s1 = k_stride_head, a.k_s2 = k_stride_pos;
   a.v_s0 = v_stride_batch, a.v_s1 = v_stride_head, a.v_s2 = v_stride_pos;
-  a.seqlens = seqlens_k;
+  // An empty cache: every sequence attends to nothing (zeros), whatever seqlens_k says.
+  a.seqlens = kv_len > 0 ? seqlens_k : nullptr;
   a.uniform_len = kv_len;
+  a.pos_cap = kv_len;
   return run_attention(c, CONTIG, a);
 }
 
