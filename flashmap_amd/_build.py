@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA accumulators stay in ArchVGPRs (no AGPR copies around the softmax).
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 
 

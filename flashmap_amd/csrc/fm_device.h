@@ -46,18 +46,38 @@ __device__ __forceinline__ f32x4_t mfma_16x16x16(u32x2_t a, u32x2_t b, f32x4_t c
                                                     __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float xor_shfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
-// Reductions over the four lanes l, l^16, l^32, l^48 (the 4 groups of one row).
+// Cross-lane pairs with gfx950's v_permlane16_swap / v_permlane32_swap: each returns,
+// in every lane l, the two values {v[l], v[l ^ 16]} (resp. {v[l], v[l ^ 32]}) in some
+// order, so a symmetric operation of the pair gives the same bits in both lanes.
+struct LanePair {
+  float a, b;
+};
+__device__ __forceinline__ LanePair pair16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ LanePair pair32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+// Reductions over the four lanes l, l^16, l^32, l^48 (the 4 groups of one row); all
+// four lanes end with identical bits.
 __device__ __forceinline__ float sum_over_groups(float v) {
-  v += xor_shfl(v, 16);
-  v += xor_shfl(v, 32);
-  return v;
+  LanePair p = pair16(v);
+  v = __fadd_rn(p.a, p.b);
+  p = pair32(v);
+  return __fadd_rn(p.a, p.b);
 }
 __device__ __forceinline__ float max_over_groups(float v) {
-  v = fmaxf(v, xor_shfl(v, 16));
-  v = fmaxf(v, xor_shfl(v, 32));
-  return v;
+  LanePair p = pair16(v);
+  v = fmaxf(p.a, p.b);
+  p = pair32(v);
+  return fmaxf(p.a, p.b);
 }
+
+// The wavefront index inside the workgroup, as a provably wave-uniform (scalar) value,
+// so that everything derived from it stays in SGPRs and uniform branches.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ u32x4_t load16(const void *p) {
   return *reinterpret_cast<const u32x4_t *>(p);
@@ -103,8 +123,7 @@ __device__ __forceinline__ void norm_rope_row(u32x4_t (&x)[D / 32], const float 
       ss = __fadd_rn(ss, __fmul_rn(o, o));
     }
   }
-  ss = __fadd_rn(ss, xor_shfl(ss, 16));
-  ss = __fadd_rn(ss, xor_shfl(ss, 32));
+  ss = sum_over_groups(ss);
   const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
   const float *cs = rope.cos + rope_row * rope.row_stride;
   const float *sn = rope.sin + rope_row * rope.row_stride;

@@ -35,7 +35,7 @@ struct KvWriteArgs {
 template <int D, bool POOL>
 __global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteArgs a) {
   constexpr int KT = D / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, g = lane >> 4;
   const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * 16 + n;
   const int64_t lh = (int64_t)a.layers * a.heads;

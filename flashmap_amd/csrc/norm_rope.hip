@@ -13,7 +13,7 @@ __global__ __launch_bounds__(256) void rms_norm_rope_kernel(
     int64_t xs_t, int64_t xs_h, int64_t os_t, int64_t os_h, const float *__restrict__ w,
     Rope rope, const int64_t *__restrict__ positions, float eps) {
   constexpr int KT = D / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, g = lane >> 4;
   const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * 16 + n;
   const bool valid = row < rows;

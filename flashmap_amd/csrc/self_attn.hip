@@ -22,7 +22,7 @@ __global__ __launch_bounds__(256) void block_self_attn_kernel(
     const int64_t *__restrict__ positions, float eps, float scale) {
   constexpr int KT = D / 32, DB = D / 16, VP = D + 4;
   __shared__ __attribute__((aligned(16))) uint16_t vstage[4][16 * VP];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, g = lane >> 4;
   const int64_t pair = (int64_t)blockIdx.x * 4 + wave;
   if (pair >= pairs) return;  // wave-uniform; no block-wide barrier follows
