@@ -6,16 +6,19 @@ K = 16 draft rows per sequence, batch 64, context lengths drawn uniform in
 [256, 8192] from seed 0, KV paged in 16-token blocks behind a randomly permuted block
 table (vLLM's FlashAttention cache layout), bf16.
 
-One call (one "step") = the fused QK-RMSNorm + RoPE prologue of the queries, the
-split-KV block attention and the log-sum-exp combine, with the step's plan (computed
-once per step and shared by every layer, like FlashAttention's scheduler metadata)
-prepared before the timed region. Inputs are resident in HBM when timing starts.
+One call (one "step") = the QK-RMSNorm + RoPE prologue of the queries (packed per
+unit by its own kernel), the split-KV block attention and the log-sum-exp combine, with
+the step's plan (computed once per step and shared by every layer, like
+FlashAttention's scheduler metadata) prepared before the timed region. Inputs are
+resident in HBM when timing starts.
 
 Prints one JSON line. `value` is microseconds per call (lower is better); the line
 also carries the achieved HBM bandwidth, a roofline record for the main attention
 kernel (algorithmic bytes / its average duration from HIP events recorded around
-each launch on its stream) and the CPU baseline (the oracle on the host cores, on a
-bounded sample of the same workload).
+each launch on its stream; `traffic` = the measured HBM bytes per launch from the
+calibrated FETCH_SIZE / WRITE_SIZE counters committed under profiles/, when present for
+the workload) and the CPU baseline (the oracle on the host cores, on a bounded sample
+of the same workload).
 """
 
 from __future__ import annotations
@@ -226,6 +229,12 @@ def main() -> int:
     kernel_ms = tot.value / max(cnt.value, 1)
 
     ab = algorithmic_bytes(inp)
+    traffic = None
+    tfile = ROOT / "profiles" / f"attn_fwd_{args.workload.split('-', 1)[0]}_paged_b{batch}.traffic.json"
+    if tfile.exists():
+        rec = json.loads(tfile.read_text())
+        if rec.get("workload") == args.workload:
+            traffic = rec["traffic_bytes"]
     us = ms * 1e3
     achieved = ab["total"] / (kernel_ms * 1e-3) / 1e9  # GB/s of the main kernel
     result = {
@@ -257,7 +266,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": ab["total"],
             "kernel_us": round(kernel_ms * 1e3, 2),
         },
