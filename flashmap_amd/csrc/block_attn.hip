@@ -801,55 +801,54 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
 }
 
 // Merge each unit's partials (one per workgroup its tiles fell to, in slots unit + w)
-// and write the bf16 output; units of empty sequences get zeros.
+// and write the bf16 output; units of empty sequences get zeros. One thread per
+// (row, 4 channels): a unit's rows * D / 4 items fill whole workgroups of 256 threads,
+// so the unit, and with it the sequence metadata, is uniform per workgroup.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
+  constexpr int C = D / 4;  // float4 chunks per row
   const int rows = a.nrb * 16;
-  const int64_t unit = blockIdx.x;
+  const int64_t per_unit = (int64_t)rows * C;  // a multiple of 256
+  const int64_t unit = (int64_t)blockIdx.x * 256 / per_unit;
+  const int item = (int)((int64_t)blockIdx.x * 256 - unit * per_unit) + threadIdx.x;
+  const int r = item / C, c = item - (item / C) * C;
   const int b = (int)(unit / a.ups);
   const int ul = (int)(unit - (int64_t)b * a.ups);
   const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
   const int64_t pre = tile_prefix(a, a.plan, b);
   const int tiles_b = (int)(tile_prefix(a, a.plan, b + 1) - pre);
   const int qlen_b = q_rows_of(a, b);
-  const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
-  const int64_t nw = a.num_wg;
-  int64_t wa = 0, wb = -1;
+  const int64_t first_tok = q_token_index(a, b, 0);
+  const int R = rg * rows + r;
+  const int gq = R / a.q_len, tq = R - gq * a.q_len;
+  if (gq >= a.group || tq >= qlen_b) return;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   if (tiles_b > 0) {
+    const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
+    const int64_t nw = a.num_wg;
     const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
-    wa = share_of(U0, total, nw);
-    wb = share_of(U0 + tiles_b - 1, total, nw);
-  }
-  constexpr int C = D / 4;  // float4 chunks per row
-  for (int idx = threadIdx.x; idx < rows * C; idx += blockDim.x) {
-    const int r = idx / C, c = idx - r * C;
-    const int R = rg * rows + r;
-    const int gq = R / a.q_len, tq = R - gq * a.q_len;
-    if (gq >= a.group || tq >= qlen_b) continue;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    if (wa == wb) {
-      acc = *reinterpret_cast<const f32x4_t *>(a.part_o + ((unit + wa) * rows + r) * D + 4 * c);
-    } else if (tiles_b > 0) {
-      float M = -INFINITY;
-      for (int64_t w = wa; w <= wb; ++w) M = fmaxf(M, a.part_lse[(unit + w) * rows + r]);
-      float den = 0.f;
-      for (int64_t w = wa; w <= wb; ++w) {
-        const int64_t slot = unit + w;
-        const float lw = a.part_lse[slot * rows + r];
-        if (lw == -INFINITY) continue;
-        const float f = __builtin_amdgcn_exp2f(lw - M);
-        acc += f * *reinterpret_cast<const f32x4_t *>(a.part_o + (slot * rows + r) * D + 4 * c);
-        den += f;
-      }
-      acc *= den > 0.f ? 1.f / den : 0.f;
+    const int64_t wa = share_of(U0, total, nw), wb = share_of(U0 + tiles_b - 1, total, nw);
+    // Running LSE merge; the loads of different segments are independent.
+    float M = -INFINITY, den = 0.f;
+#pragma unroll 4
+    for (int64_t w = wa; w <= wb; ++w) {
+      const int64_t row = (unit + w) * rows + r;
+      const float lw = a.part_lse[row];
+      const f32x4_t ow = *reinterpret_cast<const f32x4_t *>(a.part_o + row * D + 4 * c);
+      if (lw == -INFINITY) continue;
+      const float Mn = fmaxf(M, lw);
+      const float fo = __builtin_amdgcn_exp2f(M - Mn), fw = __builtin_amdgcn_exp2f(lw - Mn);
+      acc = acc * fo + ow * fw;
+      den = den * fo + fw;
+      M = Mn;
     }
-    const int64_t head = (int64_t)h * a.group + gq;
-    uint16_t *dst = a.o +
-                    (a.cu_q ? q_token_index(a, b, tq) * a.o_st
-                            : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
-                    head * a.o_sh + 4 * c;
-    *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+    acc *= den > 0.f ? 1.f / den : 0.f;
   }
+  const int64_t head = (int64_t)h * a.group + gq;
+  uint16_t *dst = a.o +
+                  (a.cu_q ? (first_tok + tq) * a.o_st : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
+                  head * a.o_sh + 4 * c;
+  *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
 }
 
 // plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(seqlens[b], 0) / TILE).
@@ -1091,10 +1090,13 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
                                           dim3(64 * sz.rp.nrb), kargs, 0, c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
+  // rows * D / 4 = 4 nrb D items per unit: a whole number of 256-thread workgroups.
+  const int64_t cblocks = units * sz.rp.nrb * 4 * c.d / 256;
+  FM_REQUIRE(cblocks < (1ll << 31), "too many units");
   if (c.d == 128)
-    attn_combine_kernel<128><<<dim3((unsigned)units), dim3(256), 0, c.stream>>>(a);
+    attn_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
   else
-    attn_combine_kernel<64><<<dim3((unsigned)units), dim3(256), 0, c.stream>>>(a);
+    attn_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }

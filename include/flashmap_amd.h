@@ -74,18 +74,21 @@ int fm_rms_norm_rope(const void *x, void *out, int64_t tokens, int32_t heads, in
  * b * *_stride_batch + t * *_stride_token. q_len(b) = cu_seqlens_q[b+1] -
  * cu_seqlens_q[b] (<= max_seqlen_q) or max_seqlen_q.
  *
- * Optional fused Q prologue: with q_norm_weight non-NULL the kernel reads the
- * pre-norm projection q and applies fm_rms_norm_rope's math itself (the rope row of
- * query token row i is q_positions[i] or i, i being the varlen row index
- * cu_seqlens_q[b] + t, or b * max_seqlen_q + t without cu_seqlens_q).
+ * Optional fused Q prologue: with q_norm_weight non-NULL the call reads the
+ * pre-norm projection q and applies fm_rms_norm_rope's math itself, bit-identically
+ * (the rope row of query token row i is q_positions[i] or i, i being the varlen row
+ * index cu_seqlens_q[b] + t, or b * max_seqlen_q + t without cu_seqlens_q).
  *
- * Split-KV: the context of all sequences is cut into equal shares over a persistent
- * grid (one share per workgroup); a sequence cut across shares is merged by a second
- * fp32 log-sum-exp pass. `plan` is fm_attn_plan's output for this step (it depends
- * only on the context lengths, so every layer of a step may share it); NULL plans
- * inside the call, in the workspace. `workspace` must hold
- * fm_attn_workspace_bytes(...) bytes for the same arguments; it is scratch that
- * concurrent calls must not share.
+ * One call enqueues three kernels: the query pass (each (sequence, KV head) unit's
+ * G x q_len rows packed contiguously in the workspace, with the prologue applied), the
+ * split-KV attention and the fp32 log-sum-exp combine that writes `out`. Split-KV:
+ * the context of all sequences is cut into equal shares over a persistent grid (one
+ * share per workgroup); every (unit, share) segment leaves an fp32 partial that the
+ * combine merges. `plan` is fm_attn_plan's output for this step (it depends only on
+ * the context lengths, so every layer of a step may share it); NULL plans inside the
+ * call, in the workspace. `workspace` must hold fm_attn_workspace_bytes(...) bytes for
+ * the same arguments (packed queries, partials, plan); it is scratch that concurrent
+ * calls must not share.
  * head_dim in {64, 128}; num_q_heads % num_kv_heads == 0.
  * A sequence with seqlen(b) == 0 gets zeros (vLLM's seqused_k = 0 rows).
  * ------------------------------------------------------------------------------ */

@@ -1,0 +1,72 @@
+"""The drop-in op layer on the CPU: the vLLM / SGLang plugin ops register under a
+namespace with the reference signatures, their fake implementations give the shapes
+and dtypes the reference's do (so torch.compile and graph capture can trace them), and
+unsupported variants fail loudly."""
+
+import pytest
+import torch
+
+from flashmap_amd import sglang as fs
+from flashmap_amd import vllm as fv
+
+META = torch.device("meta")
+
+
+def _e(*shape, dtype=torch.float32):
+    return torch.empty(*shape, dtype=dtype, device=META)
+
+
+@pytest.fixture(scope="module")
+def ns():
+    fv.register("fm_cpu_test_vllm")
+    fs.register("fm_cpu_test_sglang")
+    return torch.ops.fm_cpu_test_vllm, torch.ops.fm_cpu_test_sglang
+
+
+def test_register_is_idempotent():
+    a = fv.register("fm_cpu_test_vllm_idem")
+    assert fv.register("fm_cpu_test_vllm_idem") is a
+    assert set(a) == {"rms_norm_rope", "block_self_attention", "paged_cross_attention"}
+
+
+def test_vllm_fake_shapes(ns):
+    v, _ = ns
+    q = _e(64 * 16, 32, 128, dtype=torch.bfloat16)
+    kv = _e(100, 8, 16, 256, dtype=torch.bfloat16)
+    out = v.paged_cross_attention(q, kv, _e(65, dtype=torch.int32), _e(64, dtype=torch.int32),
+                                  _e(64, 10, dtype=torch.int32), None, None, 16, 8192, 0.088, 3)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    x = _e(10, 4, 128, dtype=torch.bfloat16)
+    assert v.rms_norm_rope(x, _e(128), _e(100, 64, 2), _e(10, dtype=torch.long), 1e-6).shape == x.shape
+    qkv = _e(3, 16, 3, 4, 128, dtype=torch.bfloat16)
+    got = v.block_self_attention(qkv, _e(128), _e(128), _e(100, 64, 2), _e(48, dtype=torch.long), 1e-6)
+    assert got.shape == (48, 512) and got.dtype == torch.bfloat16
+
+
+def test_sglang_fake_shapes(ns):
+    _, s = ns
+    qkv = _e(3, 16, 3, 4, 128, dtype=torch.bfloat16)
+    assert s.block_self_attention(qkv, _e(128), _e(128), _e(3, 16, 64, 2), 1e-6).shape == (3, 16, 4, 128)
+    q = _e(8, 16, 32, 128, dtype=torch.bfloat16)
+    kb = _e(1000, 8, 128, dtype=torch.bfloat16)
+    out = s.paged_cross_attention(q, kb, kb, _e(8, dtype=torch.int32), _e(8, 300, dtype=torch.int32), None)
+    assert out.shape == q.shape
+    x = _e(2, 16, 8, 128, dtype=torch.bfloat16)
+    assert s.rms_norm_rope(x, _e(128), _e(2, 16, 64, 2), 1e-6).shape == x.shape
+
+
+def test_unsupported_variants_raise():
+    q = torch.zeros(16, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        fv.paged_cross_attention(q, q, q, q, q, None, torch.ones(3, 1, 4), 16, 64, 0.125, 3)
+    with pytest.raises(NotImplementedError):
+        fv.write_context_kv(q, q, q, q, q, q, (1, 1, 1, 1), 16, 1e-6, scales=torch.ones(1, 2))
+    with pytest.raises(NotImplementedError):
+        fs.fused_kv_norm_rope_write(q, q, q, q, q, q, 1, 256, 64, 1e-6, is_neox_style=True)
+
+
+def test_rope_freqs_matches_oracle_table():
+    from oracle import attention as ref
+
+    pos = torch.arange(77)
+    assert torch.equal(fs.rope_freqs(pos, 128, 1e6), ref.rope_freqs(pos, 128, 1e6))
