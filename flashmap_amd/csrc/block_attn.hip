@@ -6,11 +6,11 @@
 // packed into 16-row MFMA blocks (row r = query head h*G + r / q_len at token
 // r % q_len, the GQA row convention of flashmap/sglang/verify_attention.py:77-79).
 // Each unit's context is cut into tiles of 32 positions; all units' tiles form one
-// line (sequence-major, then head, then row group) that is cut into num_wg equal
-// shares, one per workgroup of the persistent grid. A workgroup walks its share unit
-// by unit, one "segment" per unit it touches, and leaves for every segment one fp32
+// line (sequence-major, then head, then row group) that is cut into num_shares equal
+// shares, R per workgroup of the persistent grid (see replicas()). A share is walked
+// unit by unit, one "segment" per unit it touches, leaving for every segment one fp32
 // partial (O normalized by its own softmax sum, and the log-sum-exp) in slot
-// unit + workgroup, which is unique along the line. attn_combine_kernel merges each
+// unit + share, which is unique along the line. attn_combine_kernel merges each
 // unit's partials (the LSE merge of flashmap/sglang/verify_attention.py:184-233) and
 // writes the bf16 output.
 //
@@ -53,6 +53,13 @@ constexpr int TILE = 32;    // context positions per tile
 constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
 constexpr int STAGES = 3;   // LDS ring depth (tiles)
 
+// Replicas per workgroup: R independent groups of W wavefronts, each streaming its own
+// share through its own LDS ring, that meet at one barrier per tile. One workgroup per
+// CU (at head_dim 128) then keeps every resident wavefront in lockstep: co-resident
+// workgroups would instead be served oldest-first, and with equal static shares the
+// youngest would finish last, leaving a tail with a fraction of the loads in flight.
+__host__ __device__ constexpr int replicas(int w) { return w <= 6 ? 2 : 1; }
+
 enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 
 // K/V geometry of a unit, read by the streaming kernel in one scalar load whenever its
@@ -84,11 +91,11 @@ struct AttnArgs {
   int32_t uniform_len, uniform_tiles;
   int32_t batch, hkv, rgroups, ups;  // ups = hkv * rgroups units per sequence
   int32_t nrb;                       // 16-row blocks (wavefronts) per unit
-  int32_t num_wg;
+  int32_t num_shares;  // workgroups x replicas
   float scale_log2;
   const uint16_t *qp;  // packed queries: (units, 16 nrb rows, D) bf16, invalid rows 0
-  float *part_o;       // partials: (units + num_wg, 16 nrb, D) fp32
-  float *part_lse;     // (units + num_wg, 16 nrb), log2 domain (right after part_o)
+  float *part_o;       // partials: (units + num_shares, 16 nrb, D) fp32
+  float *part_lse;     // (units + num_shares, 16 nrb), log2 domain (right after part_o)
   // Query / output side (pack and combine kernels only).
   const uint16_t *q;
   int64_t q_sb, q_st, q_sh;
@@ -124,6 +131,7 @@ struct Geo {
   static constexpr int TBYTES = 128;           // page ids of the tile (generic paging)
   static constexpr int STAGE = KBYTES + VBYTES + TBYTES;
   static constexpr int SMEM = STAGES * STAGE;
+  static constexpr int QW = KT * 1024;  // one wavefront's 16 query rows, MFMA operand order
 };
 
 __device__ __forceinline__ int64_t share_start(int64_t w, int64_t total, int64_t nw) {
@@ -293,6 +301,11 @@ template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// s_waitcnt lgkmcnt(0) alone: LDS reads (and scalar loads) done, vector loads untouched.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // vmcnt 63, expcnt 7, lgkmcnt 0
 }
 
 // The same with a run-time count (generic paging only, where wavefront 0 also has
@@ -635,7 +648,7 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a) {
 }
 
 template <int LAYOUT, int W, int D>
-__global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
+__global__ __launch_bounds__(64 * W * replicas(W)) void attn_fwd_kernel(const AttnArgs a,
                                                           const int32_t *__restrict__ table,
                                                           const int32_t *__restrict__ plan,
                                                           const int32_t *__restrict__ seqlens) {
@@ -647,16 +660,32 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
   constexpr int NQ = KT;            // query-row loads per lane for a segment
   constexpr int UNIT_Q = 16 * W * D * 2;  // bytes of a unit's packed query rows
   constexpr bool TBL = LAYOUT == PAGED;
+  constexpr int R = replicas(W);
   static_assert(STAGES >= 3, "the wait schedule keeps two tiles apart");
-  __shared__ __attribute__((aligned(1024))) char smem[G::SMEM];
+  // Per replica: the K/V ring, then one query slot per wavefront.
+  constexpr int RBYTES = G::SMEM + W * G::QW;
+  __shared__ __attribute__((aligned(1024))) char smem_all[R * RBYTES];
   const SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens};
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wv = wave_id();
+  const int rep = wv / W, wave = wv - rep * W;  // replica, wavefront within it
+  // (lets the compiler prove every wavefront issues all of its K/V loads per tile)
+  __builtin_assume(wave >= 0 && wave < W && rep >= 0 && rep < R);
   const int n = lane & 15, g = lane >> 4;
+  char *const smem = smem_all + rep * RBYTES;
+  char *const qslot = smem + G::SMEM + wave * G::QW;
   const int64_t total = (int64_t)a.ups * sm.prefix(a, a.batch);
-  const int64_t T0 = share_start(blockIdx.x, total, a.num_wg);
-  const int64_t T1 = share_start((int64_t)blockIdx.x + 1, total, a.num_wg);
-  if (T0 >= T1) return;
-  const int ntiles = (int)(T1 - T0);
+  const int share = (int)blockIdx.x * R + rep;
+  const int64_t T0 = share_start(share, total, a.num_shares);
+  const int ntiles = (int)(share_start(share + 1, total, a.num_shares) - T0);
+  // Iterations of the workgroup: the largest share among its replicas (every wavefront
+  // takes part in every barrier; a replica past its share only waits at them).
+  int nloop = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t sr = (int64_t)blockIdx.x * R + r;
+    const int nr = (int)(share_start(sr + 1, total, a.num_shares) - share_start(sr, total, a.num_shares));
+    nloop = nr > nloop ? nr : nloop;
+  }
 
   // This lane's byte offsets inside a half tile for each of its loads (fast path).
   uint32_t loff[KPW];
@@ -672,9 +701,12 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
   const char *qbase = reinterpret_cast<const char *>(a.qp) + ((wave * 16 + n) * D + 8 * g) * 2;
 
   Loader ld;  // next tile to load (i + STAGES - 1)
-  ld.c = cursor_at(a, sm, T0);
-  loader_unit<LAYOUT>(table, ld);
-  loader_pages<LAYOUT>(a, ld);
+  ld.c = Cursor{0, 0, 0, 0, 0, 0, 0};
+  if (ntiles > 0) {
+    ld.c = cursor_at(a, sm, T0);
+    loader_unit<LAYOUT>(table, ld);
+    loader_pages<LAYOUT>(a, ld);
+  }
   Cursor cc = ld.c;  // tile being computed (i)
   Cursor ct = ld.c;  // generic paging: next tile whose page ids are loaded (i + STAGES)
   if (TBL) {
@@ -686,17 +718,19 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
     block_sync();
   }
 
-  // Query rows of the next segment, loaded with the first tile of its unit (the loads
-  // join that tile's group). One unit at a time: a unit whose rows could not be
-  // prefetched (the previous ones still unused) loads them when it starts.
-  u32x4_t qn[KT];
-  int qn_unit = -1;     // unit whose rows qn holds, -1: none pending
+  // Query rows of the next segment: LDS-DMA'd into this wavefront's query slot with
+  // the first tile of their unit (the KT loads join that tile's group, so the group
+  // wait covers them; loads into registers would make the compiler, which cannot
+  // follow that wait across iterations, drain every load in flight before using
+  // them). One unit at a time: a unit whose rows could not be prefetched (the slot
+  // still unread) loads them when it starts.
+  int qn_unit = -1;     // unit whose rows the slot holds or receives, -1: none pending
   uint32_t qflags = 0;  // bit j: the load group of tile i + j holds query rows
   auto prefetch_q = [&](int j) {
     if (qn_unit < 0) {
       const char *src = qbase + (uint64_t)(uint32_t)ld.c.u * UNIT_Q;
 #pragma unroll
-      for (int t = 0; t < KT; ++t) qn[t] = load16(src + 64 * t);
+      for (int t = 0; t < KT; ++t) dma16(src + 64 * t, qslot + t * 1024);
       qn_unit = ld.c.u;
       qflags |= 1u << j;
     }
@@ -718,13 +752,15 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
   gfloat *pend_o = nullptr, *pend_l = nullptr;
   int cur = 0;                        // LDS offset of tile i's stage
   int nxt = (STAGES - 1) * G::STAGE;  // LDS offset of the stage of tile i + STAGES - 1
-  for (int i = 0; i < ntiles; ++i) {
+  for (int i = 0; i < nloop; ++i) {
     // Tile i's group is complete once every later load of this wavefront is allowed to
     // be outstanding: the groups of tiles i+1 .. i+STAGES-2 (and, on wavefront 0 with
     // generic paging, the page-id loads issued after tile i's).
     const int later = ntiles - 1 - i;
     const int e = __builtin_popcount(qflags & (((1u << (STAGES - 2)) - 1) << 1));
-    if (TBL && wave == 0) {
+    if (i >= ntiles) {
+      // past this replica's share: only the barrier
+    } else if (TBL && wave == 0) {
       const int ipw = IPW + (0 < NHI ? 1 : 0);
       int nwait = ipw * min(STAGES - 2, later) + NQ * e;
       const int lo = max(i + 2, STAGES), hi = min(i + STAGES - 1, ntiles - 1);
@@ -738,6 +774,7 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
       wait_groups<IPW + 1, NQ, STAGES - 2>(later, e);
     }
     block_sync();
+    if (i >= ntiles) continue;
     if (pend) {
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
@@ -747,13 +784,18 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
     }
     if (i == 0 || cc.lt == 0) {  // a segment starts: its query rows
       if (qn_unit == cc.u) {
-#pragma unroll
-        for (int t = 0; t < KT; ++t) qf[t] = qn[t];
         qn_unit = -1;
+#pragma unroll
+        for (int t = 0; t < KT; ++t) qf[t] = *reinterpret_cast<const u32x4_t *>(qslot + t * 1024 + lane * 16);
+        // the slot may be refilled later in this iteration: the reads complete first
+        wait_lgkm0();
       } else {
+        // Not prefetched (units shorter than the ring; the slot may hold a later unit's
+        // rows in flight): straight into registers, drained here.
         const char *src = qbase + (uint64_t)(uint32_t)cc.u * UNIT_Q;
 #pragma unroll
         for (int t = 0; t < KT; ++t) qf[t] = load16(src + 64 * t);
+        wait_vm_lgkm0<0>();
       }
 #pragma unroll
       for (int t = 0; t < KT; ++t) asm volatile("" : "+v"(qf[t]));
@@ -782,7 +824,7 @@ __global__ __launch_bounds__(64 * W) void attn_fwd_kernel(const AttnArgs a,
       pend = true;
       pend_inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
       pend_lse = m + log2f(lt_sum);
-      const int64_t row = ((int64_t)cc.u + blockIdx.x) * (16 * W) + wave * 16 + n;
+      const int64_t row = ((int64_t)cc.u + (int)(blockIdx.x * R) + rep) * (16 * W) + wave * 16 + n;
       const PartPtrs pp = load_part_ptrs();
       pend_o = pp.o + row * D + 4 * g;
       pend_l = pp.lse + row;
@@ -825,7 +867,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   if (tiles_b > 0) {
     const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
-    const int64_t nw = a.num_wg;
+    const int64_t nw = a.num_shares;
     const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
     const int64_t wa = share_of(U0, total, nw), wb = share_of(U0 + tiles_b - 1, total, nw);
     // Running LSE merge; the loads of different segments are independent.
@@ -943,7 +985,8 @@ static int occupancy(AttnKernel k, int block) {
 
 struct Sizing {
   RowPlan rp;
-  int num_wg;
+  int num_wg;      // workgroups of the persistent grid
+  int num_shares;  // num_wg * replicas
   size_t plan_off, q_off, lse_off, o_off, bytes;
 };
 
@@ -959,16 +1002,18 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + TILE - 1) / TILE);
   const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
-  int64_t nw = (int64_t)info.cus * occupancy(k, 64 * sz->rp.nrb);
+  const int r = replicas(sz->rp.nrb);
+  int64_t nw = (int64_t)info.cus * occupancy(k, 64 * sz->rp.nrb * r);
   const int cap = env_int("FLASHMAP_SPLITKV_WORKGROUPS", 0);
   if (cap > 0) nw = cap;
-  const int64_t want = (tiles_bound + min_tiles - 1) / min_tiles;
-  if (want < nw) nw = want;
+  const int64_t want = (tiles_bound + min_tiles - 1) / min_tiles;  // shares worth splitting
+  if ((want + r - 1) / r < nw) nw = (want + r - 1) / r;
   if (nw < 1) nw = 1;
   sz->num_wg = (int)nw;
+  sz->num_shares = (int)nw * r;
   const size_t rows = (size_t)sz->rp.nrb * 16;
   const size_t units = (size_t)batch * ups;
-  const size_t slots = units + (size_t)nw;  // partial slot unit + workgroup
+  const size_t slots = units + (size_t)sz->num_shares;  // partial slot unit + share
   size_t off = 0;
   sz->plan_off = off;
   if (need_plan) off = align256(off + sizeof(int32_t) * ((size_t)batch + 1));
@@ -1039,7 +1084,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
     return fail(FM_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", c.ws_bytes, sz.bytes);
   FM_REQUIRE(al16(c.ws), "workspace must be 16-byte aligned");
   const int64_t units = (int64_t)c.batch * c.hkv * sz.rp.rgroups;
-  FM_REQUIRE(units + sz.num_wg < (1ll << 31) && units * sz.rp.nrb < (1ll << 33), "too many units");
+  FM_REQUIRE(units + sz.num_shares < (1ll << 31) && units * sz.rp.nrb < (1ll << 33), "too many units");
 
   a.q = (const uint16_t *)c.q;
   a.q_sb = c.q_sb, a.q_st = c.q_st, a.q_sh = c.q_sh;
@@ -1058,7 +1103,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
   a.rope = Rope{c.rope_cos, c.rope_sin, c.rope_rs, c.rope_ps, c.rope_rows};
   a.q_pos = c.q_pos;
   a.eps = c.eps;
-  a.num_wg = sz.num_wg;
+  a.num_shares = sz.num_shares;
   char *ws = (char *)c.ws;
   a.qp = (const uint16_t *)(ws + sz.q_off);
   a.part_lse = (float *)(ws + sz.lse_off);
@@ -1087,7 +1132,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
   const hipError_t lerr = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(sz.num_wg),
-                                          dim3(64 * sz.rp.nrb), kargs, 0, c.stream);
+                                          dim3(64 * sz.rp.nrb * replicas(sz.rp.nrb)), kargs, 0, c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
   // rows * D / 4 = 4 nrb D items per unit: a whole number of 256-thread workgroups.
