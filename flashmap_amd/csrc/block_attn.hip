@@ -51,14 +51,16 @@ namespace fm {
 
 constexpr int TILE = 32;    // context positions per tile
 constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
-constexpr int STAGES = 3;   // LDS ring depth (tiles)
+constexpr int STAGES = 4;   // LDS ring depth (tiles)
 
-// Replicas per workgroup: R independent groups of W wavefronts, each streaming its own
-// share through its own LDS ring, that meet at one barrier per tile. One workgroup per
-// CU (at head_dim 128) then keeps every resident wavefront in lockstep: co-resident
-// workgroups would instead be served oldest-first, and with equal static shares the
-// youngest would finish last, leaving a tail with a fraction of the loads in flight.
-__host__ __device__ constexpr int replicas(int w) { return w <= 6 ? 2 : 1; }
+// Replicas per workgroup: R independent groups of W consumer wavefronts and one producer
+// wavefront, each streaming its own share through its own LDS ring, that meet at one
+// barrier per tile. One workgroup per CU (at head_dim 128) then keeps every resident
+// wavefront in lockstep: co-resident workgroups would instead be served oldest-first, and
+// with equal static shares the youngest would finish last, leaving a tail with a
+// fraction of the loads in flight. Two replicas while the workgroup stays within 12
+// wavefronts (3 per SIMD, so up to 168 VGPRs each).
+__host__ __device__ constexpr int replicas(int w) { return 2 * (w + 1) <= 12 ? 2 : 1; }
 
 enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 
@@ -94,8 +96,9 @@ struct AttnArgs {
   int32_t num_shares;  // workgroups x replicas
   float scale_log2;
   const uint16_t *qp;  // packed queries: (units, 16 nrb rows, D) bf16, invalid rows 0
-  float *part_o;       // partials: (units + num_shares, 16 nrb, D) fp32
-  float *part_lse;     // (units + num_shares, 16 nrb), log2 domain (right after part_o)
+  uint16_t *part_o;    // partials: (units + num_shares, 16 nrb, D) fp16, rows / their scale
+  float *part_lse;     // (units + num_shares, 16 nrb, 2): log2-domain LSE, row scale
+                       // (right after part_o)
   // Query / output side (pack and combine kernels only).
   const uint16_t *q;
   int64_t q_sb, q_st, q_sh;
@@ -131,7 +134,6 @@ struct Geo {
   static constexpr int TBYTES = 128;           // page ids of the tile (generic paging)
   static constexpr int STAGE = KBYTES + VBYTES + TBYTES;
   static constexpr int SMEM = STAGES * STAGE;
-  static constexpr int QW = KT * 1024;  // one wavefront's 16 query rows, MFMA operand order
 };
 
 __device__ __forceinline__ int64_t share_start(int64_t w, int64_t total, int64_t nw) {
@@ -155,8 +157,9 @@ __device__ __forceinline__ UnitArgs load_unit_args() {
 // The partial-output pointers (part_o, part_lse: adjacent fields), re-read the same way
 // when a segment ends.
 typedef __attribute__((address_space(1))) float gfloat;  // global memory (global_* stores)
+typedef __attribute__((address_space(1))) uint16_t gu16;
 struct PartPtrs {
-  gfloat *o;
+  gu16 *o;
   gfloat *lse;
 };
 __device__ __forceinline__ PartPtrs load_part_ptrs() {
@@ -291,29 +294,25 @@ __device__ __forceinline__ Cursor cursor_at(const AttnArgs &a, const SeqMeta<VAR
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
+// K/V are read once per call: non-temporal (nt), so the stream does not displace data
+// that is reused (queries, partials, page tables) from the caches.
 __device__ __forceinline__ void dma16(const void *g, void *l) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 16, 0, /*nt*/ 2);
 }
 
-// s_waitcnt vmcnt(N) lgkmcnt(0): this wavefront's vector memory loads but the last N
-// are complete, and its LDS reads and scalar loads are done.
+// s_waitcnt vmcnt(N): this wavefront's vector memory operations but the last N are
+// complete (LDS-DMA writes included); LDS and scalar loads are left to the compiler.
 template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
+__device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// s_waitcnt lgkmcnt(0) alone: LDS reads (and scalar loads) done, vector loads untouched.
-__device__ __forceinline__ void wait_lgkm0() {
-  __builtin_amdgcn_s_waitcnt(0xF | (3 << 14) | (7 << 4));  // vmcnt 63, expcnt 7, lgkmcnt 0
-}
-
-// The same with a run-time count (generic paging only, where wavefront 0 also has
-// page-id loads in flight).
-__device__ __forceinline__ void wait_vm_lgkm0(int n) {
+// The same with a run-time count (page-id loads join the stream).
+__device__ __forceinline__ void wait_vm(int n) {
 #define FM_W(N) \
   case N:       \
-    wait_vm_lgkm0<N>(); \
+    wait_vm<N>(); \
     break;
   switch (n) {
     FM_W(0) FM_W(1) FM_W(2) FM_W(3) FM_W(4) FM_W(5) FM_W(6) FM_W(7) FM_W(8) FM_W(9)
@@ -324,35 +323,9 @@ __device__ __forceinline__ void wait_vm_lgkm0(int n) {
     FM_W(46) FM_W(47) FM_W(48) FM_W(49) FM_W(50) FM_W(51) FM_W(52) FM_W(53) FM_W(54)
     FM_W(55) FM_W(56) FM_W(57) FM_W(58) FM_W(59) FM_W(60) FM_W(61) FM_W(62)
     default:
-      wait_vm_lgkm0<0>();
+      wait_vm<0>();
   }
 #undef FM_W
-}
-
-// Wait for tile i's load group when `later` (= tiles after i in the share, at most
-// K = STAGES - 2 of them in flight) groups of IPW K/V loads may remain outstanding,
-// `e` of which also carry NQ query-row loads. Constant counts in the steady state.
-template <int IPW, int NQ, int K, int E>
-__device__ __forceinline__ void wait_groups_e(int e) {
-  if constexpr (E <= 0) {
-    wait_vm_lgkm0<IPW * K>();
-  } else {
-    if (e >= E)
-      wait_vm_lgkm0<IPW * K + NQ * E>();
-    else
-      wait_groups_e<IPW, NQ, K, E - 1>(e);
-  }
-}
-template <int IPW, int NQ, int K>
-__device__ __forceinline__ void wait_groups(int later, int e) {
-  if constexpr (K <= 0) {
-    wait_vm_lgkm0<0>();
-  } else {
-    if (later >= K)
-      wait_groups_e<IPW, NQ, K, K>(e);
-    else
-      wait_groups<IPW, NQ, K - 1>(later, e);
-  }
 }
 
 __device__ __forceinline__ void block_sync() {
@@ -360,39 +333,45 @@ __device__ __forceinline__ void block_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// Generic paging (page size not a multiple of 16, e.g. SGLang's token pool): DMA the
-// page ids of the tile's 32 positions (clamped to the sequence) into the stage's table
-// slot, one dword per lane, issued by wavefront 0 a tile ahead of the K/V loads.
-template <int D>
-__device__ __forceinline__ void issue_table(const AttnArgs &a, const int32_t *__restrict__ table,
-                                            const Cursor &c, char *stage, int lane) {
+// Paged layouts: DMA the page ids a tile's loads need into the stage's id slot, one
+// dword per lane, issued in the load stream ahead of the tile's K/V loads (so their
+// latency hides like that of K/V and no scalar load waits in the loop). Pages of 16
+// positions or a multiple: the pages of the two 16-position halves; otherwise (e.g.
+// SGLang's token pool): the page of each of the 32 positions. Positions are clamped
+// to the sequence, columns to the table.
+template <int LAYOUT, int D>
+__device__ __forceinline__ void issue_ids(const AttnArgs &a, const int32_t *__restrict__ table,
+                                          const Cursor &c, char *stage, int lane) {
   using G = Geo<D>;
-  if (lane < 32) {
+  const int32_t *row = table + (int64_t)c.b * a.u.table_stride;
+  const int last = c.L - 1 > 0 ? c.L - 1 : 0;
+  if (LAYOUT == PAGED16) {
+    if (lane < 2) {
+      int p = c.lt * TILE + 16 * lane;
+      p = p < last ? p : last;
+      const uint32_t col = min((uint32_t)p >> a.page_shift, a.col_last);
+      __builtin_amdgcn_global_load_lds(row + col, (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4, 0, 0);
+    }
+  } else if (lane < 32) {
     int p = c.lt * TILE + lane;
-    p = p < c.L ? p : c.L - 1;
-    p = p > 0 ? p : 0;
+    p = p < last ? p : last;
     int64_t col = a.page_size == 1 ? p : p / a.page_size;
     col = col < a.table_width ? col : a.table_width - 1;
-    __builtin_amdgcn_global_load_lds(table + (int64_t)c.b * a.u.table_stride + col,
-                                     (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(row + col, (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4, 0, 0);
   }
 }
 
-// Scalar state of the K/V stream: the next tile to load, the K/V bases of its unit
-// (CONTIG: sequence b, head h at position 0; paged: head h of page 0), the block-table
-// row of its sequence and, for 16-aligned pages, the pages of its two 16-position halves
-// (plain uniform loads, so scalar, issued a tile before use and clamped into the pool).
+// Scalar state of the K/V stream: the next tile to load and the K/V bases of its unit
+// (CONTIG: sequence b, head h at position 0; paged: head h of page 0).
 struct Loader {
   Cursor c;
   int lim;  // positions of the unit that may be read unclamped (CONTIG: below pos_cap too)
   int cap;  // CONTIG: positions the K/V tensors hold
   const char *kb, *vb;
-  const int32_t *trow;
-  uint32_t p0, p1;
 };
 
 template <int LAYOUT>
-__device__ __forceinline__ void loader_unit(const int32_t *__restrict__ table, Loader &ld) {
+__device__ __forceinline__ void loader_unit(Loader &ld) {
   const UnitArgs ua = load_unit_args();
   const int64_t h = ld.c.h;
   if (LAYOUT == CONTIG) {
@@ -404,31 +383,13 @@ __device__ __forceinline__ void loader_unit(const int32_t *__restrict__ table, L
     ld.lim = ld.c.L;
     ld.kb = reinterpret_cast<const char *>(ua.k + h * ua.k_s1);
     ld.vb = reinterpret_cast<const char *>(ua.v + h * ua.v_s1);
-    ld.trow = table + (int64_t)ld.c.b * ua.table_stride;
   }
 }
 
 template <int LAYOUT>
-__device__ __forceinline__ void loader_pages(const AttnArgs &a, Loader &ld) {
-  if (LAYOUT != PAGED16) return;
-  const int pos0 = ld.c.lt * TILE;
-  const int last = ld.c.L - 1 > 0 ? ld.c.L - 1 : 0;
-  const uint32_t pa = (uint32_t)(pos0 < last ? pos0 : last);
-  const uint32_t pb = (uint32_t)(pos0 + 16 < last ? pos0 + 16 : last);
-  const uint32_t ca = min(pa >> a.page_shift, a.col_last), cb = min(pb >> a.page_shift, a.col_last);
-  // The block table is read-only during the call: read through the constant address
-  // space, the loads are scalar and their wait is left to the first use (next tile).
-  typedef const __attribute__((address_space(4))) int32_t cint32_t;
-  cint32_t *row = (cint32_t *)ld.trow;
-  ld.p0 = (uint32_t)row[ca];  // clamped where used (next tile)
-  ld.p1 = (uint32_t)row[cb];
-}
-
-template <int LAYOUT>
 __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<LAYOUT != CONTIG> &sm,
-                                               const int32_t *__restrict__ table, Loader &ld) {
-  if (cursor_next(a, sm, ld.c)) loader_unit<LAYOUT>(table, ld);
-  loader_pages<LAYOUT>(a, ld);
+                                               Loader &ld) {
+  if (cursor_next(a, sm, ld.c)) loader_unit<LAYOUT>(ld);
 }
 
 // Row (within the tile) and channel offset of this lane's k-th load of a tile, and
@@ -457,6 +418,12 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
   using G = Geo<D>;
   constexpr int KPW = (G::NI + W - 1) / W;
   const int pos0 = ld.c.lt * TILE;
+  const int32_t *ids = reinterpret_cast<const int32_t *>(stage + G::KBYTES + G::VBYTES);
+  uint32_t p0 = 0, p1 = 0;  // PAGED16: pages of the two halves (negative ids wrap high)
+  if (LAYOUT == PAGED16) {
+    p0 = min((uint32_t)__builtin_amdgcn_readfirstlane(ids[0]), a.page_last);
+    p1 = min((uint32_t)__builtin_amdgcn_readfirstlane(ids[1]), a.page_last);
+  }
   if (LAYOUT != PAGED && pos0 + TILE <= ld.lim) {
     const char *kh[2], *vh[2];  // first rows of the two halves
     if (LAYOUT == CONTIG) {
@@ -466,7 +433,6 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
       vh[1] = vh[0] + 16 * a.v_tok_b;
     } else {
       const uint32_t in0 = (uint32_t)pos0 & a.page_mask, in1 = (uint32_t)(pos0 + 16) & a.page_mask;
-      const uint32_t p0 = min(ld.p0, a.page_last), p1 = min(ld.p1, a.page_last);  // negative ids wrap high
       kh[0] = ld.kb + (uint64_t)p0 * a.k_page_b + in0 * a.k_tok_b;
       vh[0] = ld.vb + (uint64_t)p0 * a.v_page_b + in0 * a.v_tok_b;
       kh[1] = ld.kb + (uint64_t)p1 * a.k_page_b + in1 * a.k_tok_b;
@@ -487,7 +453,6 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
   }
   int last = ld.c.L - 1 - pos0;  // last valid row of the tile
   last = last > 0 ? last : 0;     // (never negative, even for a plan that disagrees with L)
-  const int32_t *tbl = reinterpret_cast<const int32_t *>(stage + G::KBYTES + G::VBYTES);
 #pragma unroll
   for (int k = 0; k < KPW; ++k) {
     const int i = wave + k * W;
@@ -504,10 +469,10 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
       const int pc = p < ld.cap ? p : ld.cap - 1;
       off = (uint64_t)(uint32_t)pc * tok_b;
     } else if (LAYOUT == PAGED16) {
-      const uint32_t page = min(row >= 16 ? ld.p1 : ld.p0, a.page_last);
+      const uint32_t page = row >= 16 ? p1 : p0;
       off = (uint64_t)page * (isk ? a.k_page_b : a.v_page_b) + ((uint32_t)p & a.page_mask) * tok_b;
     } else {
-      const uint32_t page = min((uint32_t)tbl[row], a.page_last);
+      const uint32_t page = min((uint32_t)ids[row], a.page_last);
       const uint32_t in_page = a.page_size == 1 ? 0u : (uint32_t)(p - (p / a.page_size) * a.page_size);
       off = (uint64_t)page * (isk ? a.k_page_b : a.v_page_b) + in_page * tok_b;
     }
@@ -647,32 +612,57 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a) {
   for (int t = 0; t < KT; ++t) store16(dst + 32 * t, valid ? qf[t] : u32x4_t{0, 0, 0, 0});
 }
 
+// Store a segment's partial for this wavefront's 16 rows: O = acc * inv as fp16 of O /
+// scale, scale = the row's largest |O| (so every value is within [-1, 1] and keeps 11
+// significant bits wherever the row's magnitude lies), and (lse, scale) per row.
+template <int D>
+__device__ __forceinline__ void store_partial(const f32x4_t (&acc)[D / 16], float inv, float lse,
+                                              int64_t row, int g) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+  float mx = 0.f;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fabsf(acc[db][q]));
+  mx = max_over_groups(mx) * inv;
+  const float sc = mx > 0.f ? mx : 1.f;
+  const float k = inv / sc;
+  const PartPtrs pp = load_part_ptrs();
+  gu16 *dst = pp.o + row * D + 4 * g;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+    *reinterpret_cast<__attribute__((address_space(1))) u32x2_t *>(dst + 16 * db) =
+        u32x2_t{pack_f16x2(acc[db][0] * k, acc[db][1] * k), pack_f16x2(acc[db][2] * k, acc[db][3] * k)};
+  if (g == 0) *reinterpret_cast<__attribute__((address_space(1))) f32x2_t *>(pp.lse + 2 * row) = f32x2_t{lse, sc};
+}
+
+// One workgroup = R replicas x (W consumer wavefronts + 1 producer wavefront).
+//
+// The producer issues every K/V load of its replica (LDS-DMA into the ring, plus the page
+// ids with generic paging) and alone waits on vmcnt, with counts fixed by construction.
+// The consumers read LDS, compute and store their partials; their own vector memory
+// queue holds only their query-row loads (issued two tiles ahead of a unit) and partial
+// stores. One barrier per tile hands stage i from the producer (its loads complete) to
+// the consumers and stage i-1 back (their reads of it done).
 template <int LAYOUT, int W, int D>
-__global__ __launch_bounds__(64 * W * replicas(W)) void attn_fwd_kernel(const AttnArgs a,
-                                                          const int32_t *__restrict__ table,
-                                                          const int32_t *__restrict__ plan,
-                                                          const int32_t *__restrict__ seqlens) {
+__global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
+    const AttnArgs a, const int32_t *__restrict__ table, const int32_t *__restrict__ plan,
+    const int32_t *__restrict__ seqlens) {
   using G = Geo<D>;
   constexpr int KT = D / 32;
-  constexpr int KPW = (G::NI + W - 1) / W;
-  // K/V loads per tile of wavefront w: IPW + 1 for w < NHI, else IPW.
-  constexpr int IPW = G::NI / W, NHI = G::NI % W;
-  constexpr int NQ = KT;            // query-row loads per lane for a segment
   constexpr int UNIT_Q = 16 * W * D * 2;  // bytes of a unit's packed query rows
-  constexpr bool TBL = LAYOUT == PAGED;
+  constexpr bool IDS = LAYOUT != CONTIG;  // page ids join the load stream
   constexpr int R = replicas(W);
-  static_assert(STAGES >= 3, "the wait schedule keeps two tiles apart");
-  // Per replica: the K/V ring, then one query slot per wavefront.
-  constexpr int RBYTES = G::SMEM + W * G::QW;
-  __shared__ __attribute__((aligned(1024))) char smem_all[R * RBYTES];
+  constexpr int S = STAGES;
+  static_assert((S & (S - 1)) == 0 && S >= 3, "ring depth: a power of two >= 3");
+  static_assert((S - 2) * G::NI + (S - 2) < 64, "vmcnt holds 6 bits");
+  __shared__ __attribute__((aligned(1024))) char smem_all[R * G::SMEM];
   const SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens};
   const int lane = threadIdx.x & 63, wv = wave_id();
-  const int rep = wv / W, wave = wv - rep * W;  // replica, wavefront within it
-  // (lets the compiler prove every wavefront issues all of its K/V loads per tile)
-  __builtin_assume(wave >= 0 && wave < W && rep >= 0 && rep < R);
+  const int rep = wv / (W + 1), wave = wv - rep * (W + 1);  // replica; W = the producer
+  __builtin_assume(wave >= 0 && wave <= W && rep >= 0 && rep < R);
   const int n = lane & 15, g = lane >> 4;
-  char *const smem = smem_all + rep * RBYTES;
-  char *const qslot = smem + G::SMEM + wave * G::QW;
+  char *const smem = smem_all + rep * G::SMEM;
   const int64_t total = (int64_t)a.ups * sm.prefix(a, a.batch);
   const int share = (int)blockIdx.x * R + rep;
   const int64_t T0 = share_start(share, total, a.num_shares);
@@ -686,174 +676,159 @@ __global__ __launch_bounds__(64 * W * replicas(W)) void attn_fwd_kernel(const At
     const int nr = (int)(share_start(sr + 1, total, a.num_shares) - share_start(sr, total, a.num_shares));
     nloop = nr > nloop ? nr : nloop;
   }
+  Cursor cc = Cursor{0, 0, 0, 0, 0, 0, 0};  // tile being computed (i)
+  if (ntiles > 0) cc = cursor_at(a, sm, T0);
 
-  // This lane's byte offsets inside a half tile for each of its loads (fast path).
-  uint32_t loff[KPW];
+  if (wave == W) {
+    // ------------------------------------------------------------------ producer
+    // Issue order: K/V of tile t (NI loads) at iteration t - (S - 1) and, with paged
+    // layouts, the page ids of tile t + S - 1 right before them, so that the wait for
+    // tile i's group also completes the ids that the loads of tile i + S - 1 read.
+    uint32_t loff[G::NI];  // byte offsets inside a half tile of this lane's loads
 #pragma unroll
-  for (int k = 0; k < KPW; ++k) {
-    const int i = wave + k * W;
-    int row = 0, coff = 0, dst = 0;
-    bool isk = true;
-    if (i < G::NI) load_slot<D>(i, lane, row, coff, isk, dst);
-    loff[k] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + 2u * (uint32_t)coff;
+    for (int i = 0; i < G::NI; ++i) {
+      int row, coff, dst;
+      bool isk;
+      load_slot<D>(i, lane, row, coff, isk, dst);
+      loff[i] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + 2u * (uint32_t)coff;
+    }
+    Loader ld;  // next tile to load (i + S - 1)
+    ld.c = cc;
+    if (ntiles > 0) loader_unit<LAYOUT>(ld);
+    Cursor ct = cc;  // paged layouts: next tile whose page ids are loaded
+    auto stage = [&](int t) { return smem + (t & (S - 1)) * G::STAGE; };
+    if (IDS) {
+      for (int j = 0; j < S && j < ntiles; ++j) {
+        issue_ids<LAYOUT, D>(a, table, ct, stage(j), lane);
+        if (j + 1 < ntiles) cursor_next(a, sm, ct);
+      }
+      wait_vm<0>();
+    }
+    for (int j = 0; j < S - 1 && j < ntiles; ++j) {
+      issue_kv<LAYOUT, D, 1>(a, ld, stage(j), 0, lane, loff);
+      if (j + 1 < ntiles) loader_advance<LAYOUT>(a, sm, ld);
+      if (IDS && j + S <= 2 * S - 3 && j + S < ntiles) {
+        issue_ids<LAYOUT, D>(a, table, ct, stage(j + S), lane);
+        cursor_next(a, sm, ct);
+      }
+    }
+    for (int i = 0; i < nloop; ++i) {
+      // Tile i's group is complete once only what was issued after it may be
+      // outstanding: the groups of tiles i+1 .. i+S-2 and (paged layouts) the page ids
+      // of tiles i+S .. i+2S-3.
+      if (i < ntiles) {
+        const int later = ntiles - 1 - i;
+        if (IDS && later >= 2 * S - 3) {
+          wait_vm<(G::NI + 1) * (S - 2)>();
+        } else if (IDS) {
+          int nwait = G::NI * (later < S - 2 ? later : S - 2);
+          const int ids = later - (S - 1);  // tiles at or after i + S
+          nwait += ids <= 0 ? 0 : (ids < S - 2 ? ids : S - 2);
+          wait_vm(nwait);
+        } else if (later >= S - 2) {
+          wait_vm<G::NI *(S - 2)>();
+        } else if (S > 3 && later == 1) {
+          wait_vm<G::NI>();
+        } else {
+          wait_vm<0>();
+        }
+      }
+      block_sync();
+      if (i >= ntiles) continue;
+      if (i + S - 1 < ntiles) {
+        if (IDS && i + 2 * S - 2 < ntiles) {
+          issue_ids<LAYOUT, D>(a, table, ct, stage(i + 2 * S - 2), lane);
+          cursor_next(a, sm, ct);
+        }
+        issue_kv<LAYOUT, D, 1>(a, ld, stage(i + S - 1), 0, lane, loff);
+        if (i + S < ntiles) loader_advance<LAYOUT>(a, sm, ld);
+      }
+    }
+    return;
   }
-  // This lane's query channels inside a unit's packed rows.
+
+  // ------------------------------------------------------------------- consumers
+  typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
   const char *qbase = reinterpret_cast<const char *>(a.qp) + ((wave * 16 + n) * D + 8 * g) * 2;
-
-  Loader ld;  // next tile to load (i + STAGES - 1)
-  ld.c = Cursor{0, 0, 0, 0, 0, 0, 0};
-  if (ntiles > 0) {
-    ld.c = cursor_at(a, sm, T0);
-    loader_unit<LAYOUT>(table, ld);
-    loader_pages<LAYOUT>(a, ld);
-  }
-  Cursor cc = ld.c;  // tile being computed (i)
-  Cursor ct = ld.c;  // generic paging: next tile whose page ids are loaded (i + STAGES)
-  if (TBL) {
-    for (int j = 0; j < STAGES && j < ntiles; ++j) {
-      if (wave == 0) issue_table<D>(a, table, ct, smem + j * G::STAGE, lane);
-      if (j + 1 < ntiles) cursor_next(a, sm, ct);
-    }
-    wait_vm_lgkm0<0>();
-    block_sync();
-  }
-
-  // Query rows of the next segment: LDS-DMA'd into this wavefront's query slot with
-  // the first tile of their unit (the KT loads join that tile's group, so the group
-  // wait covers them; loads into registers would make the compiler, which cannot
-  // follow that wait across iterations, drain every load in flight before using
-  // them). One unit at a time: a unit whose rows could not be prefetched (the slot
-  // still unread) loads them when it starts.
-  int qn_unit = -1;     // unit whose rows the slot holds or receives, -1: none pending
-  uint32_t qflags = 0;  // bit j: the load group of tile i + j holds query rows
-  auto prefetch_q = [&](int j) {
-    if (qn_unit < 0) {
-      const char *src = qbase + (uint64_t)(uint32_t)ld.c.u * UNIT_Q;
+  auto qsrc = [&](int u) { return qbase + (uint64_t)(uint32_t)u * UNIT_Q; };
+  // Query rows of a unit are loaded into qn at the iteration of the tile two ahead of
+  // its first (cq walks there), one unit at a time; a unit whose rows could not be
+  // loaded ahead (after a unit of one or two tiles) loads them when it starts.
+  Cursor cq = cc;
+  int qn_unit = -1;
+  u32x4_t qn[KT], qf[KT];
+  if (1 < ntiles) {
+    cursor_next(a, sm, cq);
+    if (cq.lt == 0) {
 #pragma unroll
-      for (int t = 0; t < KT; ++t) dma16(src + 64 * t, qslot + t * 1024);
-      qn_unit = ld.c.u;
-      qflags |= 1u << j;
+      for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cq.u) + 64 * t);
+      qn_unit = cq.u;
     }
-  };
-
-  for (int j = 0; j < STAGES - 1 && j < ntiles; ++j) {
-    if (j == 0 || ld.c.lt == 0) prefetch_q(j);
-    issue_kv<LAYOUT, D, W>(a, ld, smem + j * G::STAGE, wave, lane, loff);
-    if (j + 1 < ntiles) loader_advance<LAYOUT>(a, sm, table, ld);
   }
-
-  u32x4_t qf[KT];
   f32x4_t acc[G::DB];
   float m = -INFINITY, l = 0.f;
-  // Output of the segment ended last iteration, stored after the next wait so that its
-  // stores do not sit in the vector memory queue in front of that wait.
+  // The partial of the segment that ended last iteration, stored once the next
+  // segment's query rows are in (stores issued ahead of them would be waited for too).
   bool pend = false;
   float pend_inv = 0.f, pend_lse = 0.f;
-  gfloat *pend_o = nullptr, *pend_l = nullptr;
-  int cur = 0;                        // LDS offset of tile i's stage
-  int nxt = (STAGES - 1) * G::STAGE;  // LDS offset of the stage of tile i + STAGES - 1
+  int64_t pend_row = 0;
   for (int i = 0; i < nloop; ++i) {
-    // Tile i's group is complete once every later load of this wavefront is allowed to
-    // be outstanding: the groups of tiles i+1 .. i+STAGES-2 (and, on wavefront 0 with
-    // generic paging, the page-id loads issued after tile i's).
-    const int later = ntiles - 1 - i;
-    const int e = __builtin_popcount(qflags & (((1u << (STAGES - 2)) - 1) << 1));
-    if (i >= ntiles) {
-      // past this replica's share: only the barrier
-    } else if (TBL && wave == 0) {
-      const int ipw = IPW + (0 < NHI ? 1 : 0);
-      int nwait = ipw * min(STAGES - 2, later) + NQ * e;
-      const int lo = max(i + 2, STAGES), hi = min(i + STAGES - 1, ntiles - 1);
-      nwait += hi >= lo ? hi - lo + 1 : 0;
-      // page ids of tile i + STAGES - 1 (issued last iteration, before its loads)
-      if (i >= 1 && i + STAGES - 1 < ntiles) nwait = min(nwait, ipw + ((qflags >> (STAGES - 2)) & 1) * NQ);
-      wait_vm_lgkm0(nwait);
-    } else if (NHI == 0 || wave >= NHI) {
-      wait_groups<IPW, NQ, STAGES - 2>(later, e);
-    } else {
-      wait_groups<IPW + 1, NQ, STAGES - 2>(later, e);
-    }
     block_sync();
     if (i >= ntiles) continue;
-    if (pend) {
-#pragma unroll
-      for (int db = 0; db < G::DB; ++db)
-        *reinterpret_cast<__attribute__((address_space(1))) f32x4_t *>(pend_o + 16 * db) = acc[db] * pend_inv;
-      if (g == 0) *pend_l = pend_lse;
-      pend = false;
-    }
     if (i == 0 || cc.lt == 0) {  // a segment starts: its query rows
       if (qn_unit == cc.u) {
+#pragma unroll
+        for (int t = 0; t < KT; ++t) qf[t] = qn[t];
         qn_unit = -1;
-#pragma unroll
-        for (int t = 0; t < KT; ++t) qf[t] = *reinterpret_cast<const u32x4_t *>(qslot + t * 1024 + lane * 16);
-        // the slot may be refilled later in this iteration: the reads complete first
-        wait_lgkm0();
       } else {
-        // Not prefetched (units shorter than the ring; the slot may hold a later unit's
-        // rows in flight): straight into registers, drained here.
-        const char *src = qbase + (uint64_t)(uint32_t)cc.u * UNIT_Q;
 #pragma unroll
-        for (int t = 0; t < KT; ++t) qf[t] = load16(src + 64 * t);
-        wait_vm_lgkm0<0>();
+        for (int t = 0; t < KT; ++t) qf[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
       }
 #pragma unroll
       for (int t = 0; t < KT; ++t) asm volatile("" : "+v"(qf[t]));
+      if (pend) {
+        store_partial<D>(acc, pend_inv, pend_lse, pend_row, g);
+        pend = false;
+      }
 #pragma unroll
       for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       m = -INFINITY;
       l = 0.f;
     }
-    if (TBL && i + STAGES < ntiles) {
-      if (wave == 0) issue_table<D>(a, table, ct, smem + cur, lane);  // tile i + STAGES
-      cursor_next(a, sm, ct);
+    // the unit starting two tiles ahead: its query rows
+    if (i + 2 < ntiles) {
+      cursor_next(a, sm, cq);
+      if (qn_unit < 0 && cq.lt == 0) {
+#pragma unroll
+        for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cq.u) + 64 * t);
+        qn_unit = cq.u;
+      }
     }
-    if (i + STAGES - 1 < ntiles) {
-      if (ld.c.lt == 0) prefetch_q(STAGES - 1);
-      issue_kv<LAYOUT, D, W>(a, ld, smem + nxt, wave, lane, loff);
-    }
-
-    compute_tile<D>(a, smem + cur, qf, acc, m, l, cc.lt * TILE, cc.L, lane);
-
-    // The loader moves on after the tile's LDS reads: its page-id loads (scalar, on
-    // the lgkm counter like LDS reads) then complete behind the P.V products.
-    if (i + STAGES < ntiles) loader_advance<LAYOUT>(a, sm, table, ld);
-
+    compute_tile<D>(a, smem + (i & (S - 1)) * G::STAGE, qf, acc, m, l, cc.lt * TILE, cc.L, lane);
     if (cc.lt == cc.tiles - 1 || i == ntiles - 1) {  // the segment ends
       const float lt_sum = sum_over_groups(l);
       pend = true;
       pend_inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
       pend_lse = m + log2f(lt_sum);
-      const int64_t row = ((int64_t)cc.u + (int)(blockIdx.x * R) + rep) * (16 * W) + wave * 16 + n;
-      const PartPtrs pp = load_part_ptrs();
-      pend_o = pp.o + row * D + 4 * g;
-      pend_l = pp.lse + row;
+      pend_row = ((int64_t)cc.u + share) * (16 * W) + wave * 16 + n;
     }
     if (i + 1 < ntiles) cursor_next(a, sm, cc);
-    qflags >>= 1;
-    cur = cur + G::STAGE == G::SMEM ? 0 : cur + G::STAGE;
-    nxt = nxt + G::STAGE == G::SMEM ? 0 : nxt + G::STAGE;
   }
-  if (pend) {
-#pragma unroll
-    for (int db = 0; db < G::DB; ++db)
-      *reinterpret_cast<__attribute__((address_space(1))) f32x4_t *>(pend_o + 16 * db) = acc[db] * pend_inv;
-    if (g == 0) *pend_l = pend_lse;
-  }
+  if (pend) store_partial<D>(acc, pend_inv, pend_lse, pend_row, g);
 }
 
-// Merge each unit's partials (one per workgroup its tiles fell to, in slots unit + w)
-// and write the bf16 output; units of empty sequences get zeros. One thread per
-// (row, 4 channels): a unit's rows * D / 4 items fill whole workgroups of 256 threads,
-// so the unit, and with it the sequence metadata, is uniform per workgroup.
+// Merge each unit's partials (one per share its tiles fell to, in slots unit + w) and
+// write the bf16 output; units of empty sequences get zeros. One workgroup per 16-row
+// block, one thread per (row, 8 channels), so the unit and its sequence metadata are
+// uniform per workgroup.
 template <int D>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
-  constexpr int C = D / 4;  // float4 chunks per row
+__global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+  constexpr int C = D / 8;  // 8-channel chunks per row
   const int rows = a.nrb * 16;
-  const int64_t per_unit = (int64_t)rows * C;  // a multiple of 256
-  const int64_t unit = (int64_t)blockIdx.x * 256 / per_unit;
-  const int item = (int)((int64_t)blockIdx.x * 256 - unit * per_unit) + threadIdx.x;
-  const int r = item / C, c = item - (item / C) * C;
+  const int64_t unit = blockIdx.x / a.nrb;
+  const int r = (int)(blockIdx.x - unit * a.nrb) * 16 + (int)threadIdx.x / C;
+  const int c = (int)threadIdx.x % C;
   const int b = (int)(unit / a.ups);
   const int ul = (int)(unit - (int64_t)b * a.ups);
   const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
@@ -864,7 +839,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
   const int R = rg * rows + r;
   const int gq = R / a.q_len, tq = R - gq * a.q_len;
   if (gq >= a.group || tq >= qlen_b) return;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   if (tiles_b > 0) {
     const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
     const int64_t nw = a.num_shares;
@@ -875,22 +850,29 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
 #pragma unroll 4
     for (int64_t w = wa; w <= wb; ++w) {
       const int64_t row = (unit + w) * rows + r;
-      const float lw = a.part_lse[row];
-      const f32x4_t ow = *reinterpret_cast<const f32x4_t *>(a.part_o + row * D + 4 * c);
-      if (lw == -INFINITY) continue;
-      const float Mn = fmaxf(M, lw);
-      const float fo = __builtin_amdgcn_exp2f(M - Mn), fw = __builtin_amdgcn_exp2f(lw - Mn);
-      acc = acc * fo + ow * fw;
-      den = den * fo + fw;
+      const f32x2_t ls = *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row);
+      const u32x4_t ow = load16(a.part_o + row * D + 8 * c);
+      if (ls[0] == -INFINITY) continue;
+      const float Mn = fmaxf(M, ls[0]);
+      const float fo = __builtin_amdgcn_exp2f(M - Mn), ew = __builtin_amdgcn_exp2f(ls[0] - Mn);
+      const float fw = ew * ls[1];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[j] = acc[j] * fo + f32x4_t{f16_lo(ow[2 * j]), f16_hi(ow[2 * j]), f16_lo(ow[2 * j + 1]),
+                                       f16_hi(ow[2 * j + 1])} * fw;
+      den = den * fo + ew;
       M = Mn;
     }
-    acc *= den > 0.f ? 1.f / den : 0.f;
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    acc[0] *= inv;
+    acc[1] *= inv;
   }
   const int64_t head = (int64_t)h * a.group + gq;
   uint16_t *dst = a.o +
                   (a.cu_q ? (first_tok + tq) * a.o_st : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
-                  head * a.o_sh + 4 * c;
-  *reinterpret_cast<u32x2_t *>(dst) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+                  head * a.o_sh + 8 * c;
+  store16(dst, u32x4_t{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+                       pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])});
 }
 
 // plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(seqlens[b], 0) / TILE).
@@ -1003,7 +985,7 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + TILE - 1) / TILE);
   const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
   const int r = replicas(sz->rp.nrb);
-  int64_t nw = (int64_t)info.cus * occupancy(k, 64 * sz->rp.nrb * r);
+  int64_t nw = (int64_t)info.cus * occupancy(k, 64 * (sz->rp.nrb + 1) * r);
   const int cap = env_int("FLASHMAP_SPLITKV_WORKGROUPS", 0);
   if (cap > 0) nw = cap;
   const int64_t want = (tiles_bound + min_tiles - 1) / min_tiles;  // shares worth splitting
@@ -1020,9 +1002,9 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->q_off = off;
   off = align256(off + sizeof(uint16_t) * units * rows * d);
   sz->lse_off = off;
-  off = align256(off + sizeof(float) * slots * rows);
+  off = align256(off + 2 * sizeof(float) * slots * rows);
   sz->o_off = off;
-  off = align256(off + sizeof(float) * slots * rows * d);
+  off = align256(off + sizeof(uint16_t) * slots * rows * d);
   sz->bytes = off;
   return FM_OK;
 }
@@ -1107,7 +1089,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
   char *ws = (char *)c.ws;
   a.qp = (const uint16_t *)(ws + sz.q_off);
   a.part_lse = (float *)(ws + sz.lse_off);
-  a.part_o = (float *)(ws + sz.o_off);
+  a.part_o = (uint16_t *)(ws + sz.o_off);
   if (a.seqlens != nullptr) {
     if (need_plan) {
       int32_t *plan = (int32_t *)(ws + sz.plan_off);
@@ -1132,16 +1114,16 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
   const hipError_t lerr = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(sz.num_wg),
-                                          dim3(64 * sz.rp.nrb * replicas(sz.rp.nrb)), kargs, 0, c.stream);
+                                          dim3(64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb)), kargs, 0, c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
-  // rows * D / 4 = 4 nrb D items per unit: a whole number of 256-thread workgroups.
-  const int64_t cblocks = units * sz.rp.nrb * 4 * c.d / 256;
+  // One workgroup of 2 D threads per 16-row block.
+  const int64_t cblocks = units * sz.rp.nrb;
   FM_REQUIRE(cblocks < (1ll << 31), "too many units");
   if (c.d == 128)
     attn_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
   else
-    attn_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
+    attn_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(128), 0, c.stream>>>(a);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
