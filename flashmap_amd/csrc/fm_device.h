@@ -107,20 +107,78 @@ __device__ __forceinline__ int64_t clamp_row(const Rope &rope, int64_t r) {
   return r;
 }
 
+// The per-lane operands of the prologue for one row in the row-quad layout (x[t] holds
+// channels 32 t + 8 g + (0..7), i.e. the pairs 16 t + 4 g + (0..3)): the norm weights
+// of those channels and the rotary cos / sin of those pairs. Loaded with 16-byte loads
+// where the table layout allows (contiguous pairs, or (cos, sin) interleaved), else per
+// element.
+template <int D>
+struct PrologueOps {
+  float w[D / 32][8];
+  float c[D / 32][4], s[D / 32][4];
+};
+
+typedef __attribute__((ext_vector_type(4), aligned(4))) float f32x4u_t;  // 4-byte aligned
+
+template <int D>
+__device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const float *__restrict__ w,
+                                                  const Rope &rope, int64_t rope_row, int g) {
+  constexpr int KT = D / 32;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const f32x4u_t lo = *reinterpret_cast<const f32x4u_t *>(w + 32 * t + 8 * g);
+    const f32x4u_t hi = *reinterpret_cast<const f32x4u_t *>(w + 32 * t + 8 * g + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ops.w[t][q] = lo[q];
+      ops.w[t][4 + q] = hi[q];
+    }
+  }
+  const float *cs = rope.cos + rope_row * rope.row_stride;
+  const float *sn = rope.sin + rope_row * rope.row_stride;
+  if (rope.pair_stride == 1) {
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const f32x4u_t cv = *reinterpret_cast<const f32x4u_t *>(cs + 16 * t + 4 * g);
+      const f32x4u_t sv = *reinterpret_cast<const f32x4u_t *>(sn + 16 * t + 4 * g);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ops.c[t][q] = cv[q];
+        ops.s[t][q] = sv[q];
+      }
+    }
+  } else if (rope.pair_stride == 2 && sn == cs + 1) {
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const f32x4u_t v0 = *reinterpret_cast<const f32x4u_t *>(cs + 32 * t + 8 * g);
+      const f32x4u_t v1 = *reinterpret_cast<const f32x4u_t *>(cs + 32 * t + 8 * g + 4);
+      ops.c[t][0] = v0[0], ops.s[t][0] = v0[1], ops.c[t][1] = v0[2], ops.s[t][1] = v0[3];
+      ops.c[t][2] = v1[0], ops.s[t][2] = v1[1], ops.c[t][3] = v1[2], ops.s[t][3] = v1[3];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t p = 16 * t + 4 * g + q;
+        ops.c[t][q] = cs[p * rope.pair_stride];
+        ops.s[t][q] = sn[p * rope.pair_stride];
+      }
+  }
+}
+
 // RMSNorm (scale rounded to bf16 before the multiply, product rounded to bf16) then
 // interleaved-pair RoPE (fp32 rotate of the bf16 normed values, rounded to bf16) of one
-// row held in the row-quad layout: x[t] holds channels 32 t + 8 g + (0..7). Every lane
-// of the wavefront must call this (the row reduction crosses lane groups). The
-// arithmetic is spelled with explicit round-to-nearest operations so that every
-// caller computes bit-identical values:
+// row held in the row-quad layout. Every lane of the wavefront must call this (the row
+// reduction crosses lane groups). The arithmetic is spelled with explicit
+// round-to-nearest operations so that every caller computes bit-identical values:
 //   r  = 1 / sqrt(sum(x^2) / D + eps)
 //   y  = bf16(x * bf16(w * r))
 //   e' = bf16(e c - o s),  o' = bf16(o c + e s)       (each product rounded)
 // Follows flashmap/modeling_flashmap.py:61-66,79-80 and flashmap/vllm/kernels.py:84-98.
 template <int D>
-__device__ __forceinline__ void norm_rope_row(u32x4_t (&x)[D / 32], const float *__restrict__ w,
-                                              float eps, const Rope &rope, int64_t rope_row,
-                                              int g) {
+__device__ __forceinline__ void norm_rope_apply(u32x4_t (&x)[D / 32], const PrologueOps<D> &ops,
+                                                float eps) {
   constexpr int KT = D / 32;
   float ss = 0.f;
 #pragma unroll
@@ -134,24 +192,29 @@ __device__ __forceinline__ void norm_rope_row(u32x4_t (&x)[D / 32], const float 
   }
   ss = sum_over_groups(ss);
   const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
-  const float *cs = rope.cos + rope_row * rope.row_stride;
-  const float *sn = rope.sin + rope_row * rope.row_stride;
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int d = 32 * t + 8 * g + 2 * q;
-      const float se = round_bf16(__fmul_rn(w[d], r));
-      const float so = round_bf16(__fmul_rn(w[d + 1], r));
+      const float se = round_bf16(__fmul_rn(ops.w[t][2 * q], r));
+      const float so = round_bf16(__fmul_rn(ops.w[t][2 * q + 1], r));
       const float e = round_bf16(__fmul_rn(bf16_lo(x[t][q]), se));
       const float o = round_bf16(__fmul_rn(bf16_hi(x[t][q]), so));
-      const float c = cs[(d >> 1) * rope.pair_stride];
-      const float s = sn[(d >> 1) * rope.pair_stride];
+      const float c = ops.c[t][q], s = ops.s[t][q];
       const float e2 = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s));
       const float o2 = __fadd_rn(__fmul_rn(o, c), __fmul_rn(e, s));
       x[t][q] = pack_bf16x2(e2, o2);
     }
   }
+}
+
+template <int D>
+__device__ __forceinline__ void norm_rope_row(u32x4_t (&x)[D / 32], const float *__restrict__ w,
+                                              float eps, const Rope &rope, int64_t rope_row,
+                                              int g) {
+  PrologueOps<D> ops;
+  load_prologue_ops<D>(ops, w, rope, rope_row, g);
+  norm_rope_apply<D>(x, ops, eps);
 }
 
 }  // namespace fm
