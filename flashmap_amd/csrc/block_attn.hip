@@ -51,7 +51,7 @@ namespace fm {
 
 constexpr int TILE = 32;    // context positions per tile
 constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
-constexpr int STAGES = 4;   // LDS ring depth (tiles)
+constexpr int STAGES = 3;   // LDS ring depth (tiles)
 
 // Replicas per workgroup: R independent groups of W consumer wavefronts and one producer
 // wavefront, each streaming its own share through its own LDS ring, that meet at one
@@ -64,8 +64,7 @@ __host__ __device__ constexpr int replicas(int w) { return 2 * (w + 1) <= 12 ? 2
 
 enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 
-// K/V geometry of a unit, read by the streaming kernel in one scalar load whenever its
-// K/V stream enters a new unit.
+// K/V geometry of the units.
 struct UnitArgs {
   const uint16_t *k;
   const uint16_t *v;
@@ -75,10 +74,9 @@ struct UnitArgs {
   int32_t pos_cap;  // CONTIG: positions the K/V tensors hold (reads are clamped below it)
   int32_t pad;
 };
-static_assert(sizeof(UnitArgs) == 64, "one s_load_dwordx16");
 
 struct AttnArgs {
-  UnitArgs u;  // first: at offset 0 of every kernel's argument segment
+  UnitArgs u;
   // Per-tile address arithmetic in 32 bits (byte strides; the host checks they fit).
   uint32_t k_tok_b, v_tok_b;    // position / token stride
   uint32_t k_page_b, v_page_b;  // paged: page (slot) stride
@@ -143,34 +141,8 @@ __device__ __forceinline__ int64_t share_of(int64_t x, int64_t total, int64_t nw
   return ((x + 1) * nw - 1) / total;
 }
 
-// The unit block of the arguments, re-read from offset 0 of the kernel argument segment
-// in one scalar load (volatile, so the compiler keeps none of it in SGPRs across the
-// tile loop).
-__device__ __forceinline__ UnitArgs load_unit_args() {
-  typedef __attribute__((ext_vector_type(16))) uint32_t u32x16_t;
-  const uint64_t base = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
-  u32x16_t v;
-  asm volatile("s_load_dwordx16 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(base));
-  return __builtin_bit_cast(UnitArgs, v);
-}
-
-// The partial-output pointers (part_o, part_lse: adjacent fields), re-read the same way
-// when a segment ends.
 typedef __attribute__((address_space(1))) float gfloat;  // global memory (global_* stores)
 typedef __attribute__((address_space(1))) uint16_t gu16;
-struct PartPtrs {
-  gu16 *o;
-  gfloat *lse;
-};
-__device__ __forceinline__ PartPtrs load_part_ptrs() {
-  typedef __attribute__((ext_vector_type(4))) uint32_t u32x4v_t;
-  const uint64_t base = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
-  u32x4v_t v;
-  asm volatile("s_load_dwordx4 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
-               : "=s"(v)
-               : "s"(base), "i"((int)offsetof(AttnArgs, part_o)));
-  return __builtin_bit_cast(PartPtrs, v);
-}
 
 // Scalar (SMEM) loads of wave-uniform metadata that no kernel of this call writes
 // (plans, lengths). Completion is awaited inside, on lgkmcnt, so the values never
@@ -222,17 +194,29 @@ struct Cursor {
   int b, h, rg, lt, tiles, L, u;
 };
 
+// Sequences whose (tile prefix, length) the streaming kernel stages in LDS at its start,
+// so that no scalar load waits on the tile path (a scalar load's wait would also hold
+// up the LDS reads around it, both counting on lgkmcnt); larger batches read them with
+// scalar loads.
+constexpr int SEQ_LDS = 1024;
+typedef __attribute__((ext_vector_type(2))) int32_t i32x2_t;
+typedef __attribute__((address_space(3))) const i32x2_t lds_i32x2_t;
+
 // Plan and lengths of the streaming kernel; VAR: known to be per-sequence (the paged
-// layouts always are), so the uniform-length fields are never read.
+// layouts always are), so the uniform-length fields are never read. tab: the staged
+// (prefix, length) of sequences 0 .. batch when staged.
 template <bool VAR>
 struct SeqMeta {
   const int32_t *plan;
   const int32_t *seqlens;
+  lds_i32x2_t *tab;
+  bool staged;
   __device__ __forceinline__ bool var() const { return VAR || plan != nullptr; }
   __device__ __forceinline__ int64_t prefix(const AttnArgs &a, int b) const {
-    return var() ? (int64_t)sload(plan + b) : (int64_t)b * a.uniform_tiles;
+    if (!var()) return (int64_t)b * a.uniform_tiles;
+    return staged ? (int64_t)tab[b][0] : (int64_t)sload(plan + b);
   }
-  // tiles(b) = prefix(b + 1) - prefix(b) and the length of sequence b, one round trip.
+  // tiles(b) = prefix(b + 1) - prefix(b) and the length of sequence b.
   __device__ __forceinline__ void seq(const AttnArgs &a, int b, int &tiles, int &L) const {
     if (!var()) {
       tiles = a.uniform_tiles;
@@ -240,7 +224,14 @@ struct SeqMeta {
       return;
     }
     int32_t p0, p1, len;
-    sload3(plan + b, seqlens + b, p0, p1, len);
+    if (staged) {
+      const i32x2_t e = tab[b];
+      p0 = e[0];
+      len = e[1];
+      p1 = tab[b + 1][0];
+    } else {
+      sload3(plan + b, seqlens + b, p0, p1, len);
+    }
     tiles = p1 - p0;
     L = len > 0 ? len : 0;
   }
@@ -371,8 +362,8 @@ struct Loader {
 };
 
 template <int LAYOUT>
-__device__ __forceinline__ void loader_unit(Loader &ld) {
-  const UnitArgs ua = load_unit_args();
+__device__ __forceinline__ void loader_unit(const AttnArgs &a, Loader &ld) {
+  const UnitArgs &ua = a.u;
   const int64_t h = ld.c.h;
   if (LAYOUT == CONTIG) {
     ld.cap = ua.pos_cap;
@@ -389,7 +380,7 @@ __device__ __forceinline__ void loader_unit(Loader &ld) {
 template <int LAYOUT>
 __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<LAYOUT != CONTIG> &sm,
                                                Loader &ld) {
-  if (cursor_next(a, sm, ld.c)) loader_unit<LAYOUT>(ld);
+  if (cursor_next(a, sm, ld.c)) loader_unit<LAYOUT>(a, ld);
 }
 
 // Row (within the tile) and channel offset of this lane's k-th load of a tile, and
@@ -612,13 +603,12 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a) {
   for (int t = 0; t < KT; ++t) store16(dst + 32 * t, valid ? qf[t] : u32x4_t{0, 0, 0, 0});
 }
 
-// Store a segment's partial for this wavefront's 16 rows: O = acc * inv as fp16 of O /
-// scale, scale = the row's largest |O| (so every value is within [-1, 1] and keeps 11
-// significant bits wherever the row's magnitude lies), and (lse, scale) per row.
+// A segment's partial for this wavefront's 16 rows: O = acc * inv as fp16 of O / scale,
+// scale = the row's largest |O| (so every value is within [-1, 1] and keeps 11
+// significant bits wherever the row's magnitude lies). h[db] holds channels
+// 16 db + 4 g .. + 3 of row n.
 template <int D>
-__device__ __forceinline__ void store_partial(const f32x4_t (&acc)[D / 16], float inv, float lse,
-                                              int64_t row, int g) {
-  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+__device__ __forceinline__ float make_partial(const f32x4_t (&acc)[D / 16], float inv, u32x2_t (&h)[D / 16]) {
   float mx = 0.f;
 #pragma unroll
   for (int db = 0; db < D / 16; ++db)
@@ -627,42 +617,124 @@ __device__ __forceinline__ void store_partial(const f32x4_t (&acc)[D / 16], floa
   mx = max_over_groups(mx) * inv;
   const float sc = mx > 0.f ? mx : 1.f;
   const float k = inv / sc;
-  const PartPtrs pp = load_part_ptrs();
-  gu16 *dst = pp.o + row * D + 4 * g;
 #pragma unroll
   for (int db = 0; db < D / 16; ++db)
-    *reinterpret_cast<__attribute__((address_space(1))) u32x2_t *>(dst + 16 * db) =
-        u32x2_t{pack_f16x2(acc[db][0] * k, acc[db][1] * k), pack_f16x2(acc[db][2] * k, acc[db][3] * k)};
-  if (g == 0) *reinterpret_cast<__attribute__((address_space(1))) f32x2_t *>(pp.lse + 2 * row) = f32x2_t{lse, sc};
+    h[db] = u32x2_t{pack_f16x2(acc[db][0] * k, acc[db][1] * k), pack_f16x2(acc[db][2] * k, acc[db][3] * k)};
+  return sc;
 }
+
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+
+// Partial slot layout in the workspace: rows (slot * 16 W + r) of D fp16, and per row
+// (lse, scale) as two floats.
+template <int D>
+__device__ __forceinline__ void store_partial_rows(const AttnArgs &a, const u32x2_t (&h)[D / 16], float lse,
+                                                   float sc, int64_t row, int g) {
+  gu16 *dst = (gu16 *)a.part_o + row * D + 4 * g;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+    *reinterpret_cast<__attribute__((address_space(1))) u32x2_t *>(dst + 16 * db) = h[db];
+  if (g == 0)
+    *reinterpret_cast<__attribute__((address_space(1))) f32x2_t *>((gfloat *)a.part_lse + 2 * row) = f32x2_t{lse, sc};
+}
+
+// The hand-off of partials from the consumers to the producer: an LDS slot of the
+// 16 W rows (D fp16 each, 16-byte chunk c of row r stored at chunk c ^ (r mod D/8), so
+// that both the consumers' 8-byte writes and the producer's 16-byte reads spread over
+// the banks), then (lse, scale) per row. The producer issues the global stores: a
+// consumer's stores would queue behind the producer's loads in the CU's memory pipeline
+// and hold every wavefront of the workgroup at the next barrier.
+template <int D, int W>
+struct OutSlot {
+  static constexpr int ROWS = 16 * W;
+  static constexpr int CH = D / 8;         // 16-byte chunks per row
+  static constexpr int OBYTES = ROWS * D * 2;
+  static constexpr int BYTES = OBYTES + ROWS * 8;
+};
+
+template <int D, int W>
+__device__ __forceinline__ void out_write(char *slot, const u32x2_t (&h)[D / 16], float lse, float sc, int wave,
+                                          int n, int g) {
+  using O = OutSlot<D, W>;
+  typedef __attribute__((address_space(3))) u32x2_t lds_u32x2_t;
+  typedef __attribute__((address_space(3))) f32x2_t lds_f32x2_t;
+  const int r = wave * 16 + n;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    const int c = 2 * db + (g >> 1);
+    *(lds_u32x2_t *)(slot + r * (2 * D) + ((c ^ (r & (O::CH - 1))) << 4) + 8 * (g & 1)) = h[db];
+  }
+  if (g == 0) *(lds_f32x2_t *)(slot + O::OBYTES + 8 * r) = f32x2_t{lse, sc};
+}
+
+template <int D, int W>
+__device__ __forceinline__ void out_store(const AttnArgs &a, const char *slot, int64_t slot_idx, int lane) {
+  using O = OutSlot<D, W>;
+  typedef __attribute__((address_space(3))) const u32x4_t lds_u32x4_t;
+  typedef __attribute__((address_space(3))) const f32x2_t lds_f32x2_t;
+  typedef __attribute__((address_space(1))) char gchar;
+  gchar *const base = (gchar *)a.part_o + slot_idx * O::OBYTES;
+  constexpr int NK = O::ROWS * O::CH / 64, BATCH = NK % 4 == 0 ? 4 : (NK % 2 == 0 ? 2 : 1);
+#pragma unroll 1
+  for (int k0 = 0; k0 < NK; k0 += BATCH) {  // a few reads in flight, few registers
+    u32x4_t v[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) v[j] = *(lds_u32x4_t *)(slot + 16 * ((k0 + j) * 64 + lane));
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int q = (k0 + j) * 64 + lane, r = q / O::CH, p = q % O::CH;
+      *(__attribute__((address_space(1))) u32x4_t *)(base + r * (2 * D) + ((p ^ (r & (O::CH - 1))) << 4)) = v[j];
+    }
+  }
+  for (int r = lane; r < O::ROWS; r += 64)
+    *reinterpret_cast<__attribute__((address_space(1))) f32x2_t *>((gfloat *)a.part_lse + 2 * (slot_idx * O::ROWS + r)) =
+        *(lds_f32x2_t *)(slot + O::OBYTES + 8 * r);
+}
+
+// LDS writes of this wavefront complete (before a barrier that publishes them).
+__device__ __forceinline__ void lds_publish() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // One workgroup = R replicas x (W consumer wavefronts + 1 producer wavefront).
 //
-// The producer issues every K/V load of its replica (LDS-DMA into the ring, plus the page
-// ids with generic paging) and alone waits on vmcnt, with counts fixed by construction.
-// The consumers read LDS, compute and store their partials; their own vector memory
-// queue holds only their query-row loads (issued two tiles ahead of a unit) and partial
-// stores. One barrier per tile hands stage i from the producer (its loads complete) to
-// the consumers and stage i-1 back (their reads of it done).
+// The producer issues every load of its replica's K/V stream (LDS-DMA into the ring, plus
+// the page ids with paged layouts), alone waits on vmcnt, with counts fixed by
+// construction, and stores the partials the consumers hand over through LDS. The
+// consumers read LDS, compute and load their query rows a unit ahead. One barrier per
+// tile hands stage i from the producer (its loads complete) to the consumers and stage
+// i-1 back (their reads of it done), and a partial written in iteration t to the
+// producer, who stores it in iteration t + 1.
 template <int LAYOUT, int W, int D>
 __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     const AttnArgs a, const int32_t *__restrict__ table, const int32_t *__restrict__ plan,
     const int32_t *__restrict__ seqlens) {
   using G = Geo<D>;
+  using O = OutSlot<D, W>;
   constexpr int KT = D / 32;
   constexpr int UNIT_Q = 16 * W * D * 2;  // bytes of a unit's packed query rows
   constexpr bool IDS = LAYOUT != CONTIG;  // page ids join the load stream
   constexpr int R = replicas(W);
   constexpr int S = STAGES;
-  static_assert((S & (S - 1)) == 0 && S >= 3, "ring depth: a power of two >= 3");
+  constexpr int RBYTES = G::SMEM + O::BYTES;  // per replica: the ring, then the out slot
+  static_assert(S >= 3, "the wait schedule keeps one group between tiles");
   static_assert((S - 2) * G::NI + (S - 2) < 64, "vmcnt holds 6 bits");
-  __shared__ __attribute__((aligned(1024))) char smem_all[R * G::SMEM];
-  const SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens};
+  __shared__ __attribute__((aligned(1024))) char smem_all[R * RBYTES];
+  __shared__ i32x2_t seq_tab[SEQ_LDS + 1];
+  SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens, (lds_i32x2_t *)seq_tab, false};
+  if (sm.var() && a.batch <= SEQ_LDS) {  // uniform: every wavefront takes the barrier
+    for (int j = threadIdx.x; j <= a.batch; j += blockDim.x) {
+      const int len = j < a.batch ? seqlens[j] : 0;
+      seq_tab[j] = i32x2_t{plan[j], len};
+    }
+    lds_publish();
+    block_sync();
+    sm.staged = true;
+  }
   const int lane = threadIdx.x & 63, wv = wave_id();
   const int rep = wv / (W + 1), wave = wv - rep * (W + 1);  // replica; W = the producer
   __builtin_assume(wave >= 0 && wave <= W && rep >= 0 && rep < R);
   const int n = lane & 15, g = lane >> 4;
-  char *const smem = smem_all + rep * G::SMEM;
+  char *const smem = smem_all + rep * RBYTES;
+  char *const out = smem + G::SMEM;
   const int64_t total = (int64_t)a.ups * sm.prefix(a, a.batch);
   const int share = (int)blockIdx.x * R + rep;
   const int64_t T0 = share_start(share, total, a.num_shares);
@@ -678,12 +750,18 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   }
   Cursor cc = Cursor{0, 0, 0, 0, 0, 0, 0};  // tile being computed (i)
   if (ntiles > 0) cc = cursor_at(a, sm, T0);
+  auto stage = [&](int t) { return smem + (t % S) * G::STAGE; };
+  // A segment ends at tile t when t is its unit's last or the share's last tile. Its
+  // partial goes through the out slot unless tile t - 1 ended one too (the slot may
+  // still be read then); the consumers then store it themselves.
 
   if (wave == W) {
     // ------------------------------------------------------------------ producer
     // Issue order: K/V of tile t (NI loads) at iteration t - (S - 1) and, with paged
     // layouts, the page ids of tile t + S - 1 right before them, so that the wait for
     // tile i's group also completes the ids that the loads of tile i + S - 1 read.
+    // Partial stores only ever make a wait more conservative (stores complete out of
+    // order with loads; loads among themselves in order).
     uint32_t loff[G::NI];  // byte offsets inside a half tile of this lane's loads
 #pragma unroll
     for (int i = 0; i < G::NI; ++i) {
@@ -694,9 +772,16 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     }
     Loader ld;  // next tile to load (i + S - 1)
     ld.c = cc;
-    if (ntiles > 0) loader_unit<LAYOUT>(ld);
+    if (ntiles > 0) loader_unit<LAYOUT>(a, ld);
     Cursor ct = cc;  // paged layouts: next tile whose page ids are loaded
-    auto stage = [&](int t) { return smem + (t & (S - 1)) * G::STAGE; };
+    Cursor pc = cc;  // the tile whose partial (if any) is stored next
+    bool pc_prev_end = false;
+    auto handoff = [&](int t) {  // after the barrier that follows tile t
+      const bool end = pc.lt == pc.tiles - 1 || t == ntiles - 1;
+      if (end && !pc_prev_end) out_store<D, W>(a, out, (int64_t)pc.u + share, lane);
+      pc_prev_end = end;
+      if (t + 1 < ntiles) cursor_next(a, sm, pc);
+    };
     if (IDS) {
       for (int j = 0; j < S && j < ntiles; ++j) {
         issue_ids<LAYOUT, D>(a, table, ct, stage(j), lane);
@@ -734,6 +819,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
         }
       }
       block_sync();
+      if (i >= 1 && i - 1 < ntiles) handoff(i - 1);
       if (i >= ntiles) continue;
       if (i + S - 1 < ntiles) {
         if (IDS && i + 2 * S - 2 < ntiles) {
@@ -744,6 +830,8 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
         if (i + S < ntiles) loader_advance<LAYOUT>(a, sm, ld);
       }
     }
+    block_sync();
+    if (ntiles > 0 && ntiles == nloop) handoff(ntiles - 1);
     return;
   }
 
@@ -751,27 +839,22 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
   const char *qbase = reinterpret_cast<const char *>(a.qp) + ((wave * 16 + n) * D + 8 * g) * 2;
   auto qsrc = [&](int u) { return qbase + (uint64_t)(uint32_t)u * UNIT_Q; };
-  // Query rows of a unit are loaded into qn at the iteration of the tile two ahead of
-  // its first (cq walks there), one unit at a time; a unit whose rows could not be
-  // loaded ahead (after a unit of one or two tiles) loads them when it starts.
-  Cursor cq = cc;
+  // Query rows of the next unit are loaded into qn as soon as the current unit's are
+  // taken (the first unit's before the producer's first loads are queued ahead of
+  // them), so their latency hides behind a whole unit. The next unit on the line is
+  // u + 1 unless sequences without context lie between; then the rows are loaded when
+  // the unit starts.
+  const int units = a.batch * a.ups;
   int qn_unit = -1;
   u32x4_t qn[KT], qf[KT];
-  if (1 < ntiles) {
-    cursor_next(a, sm, cq);
-    if (cq.lt == 0) {
+  if (ntiles > 0) {
 #pragma unroll
-      for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cq.u) + 64 * t);
-      qn_unit = cq.u;
-    }
+    for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
+    qn_unit = cc.u;
   }
   f32x4_t acc[G::DB];
   float m = -INFINITY, l = 0.f;
-  // The partial of the segment that ended last iteration, stored once the next
-  // segment's query rows are in (stores issued ahead of them would be waited for too).
-  bool pend = false;
-  float pend_inv = 0.f, pend_lse = 0.f;
-  int64_t pend_row = 0;
+  bool prev_end = false;
   for (int i = 0; i < nloop; ++i) {
     block_sync();
     if (i >= ntiles) continue;
@@ -779,42 +862,42 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       if (qn_unit == cc.u) {
 #pragma unroll
         for (int t = 0; t < KT; ++t) qf[t] = qn[t];
-        qn_unit = -1;
       } else {
 #pragma unroll
         for (int t = 0; t < KT; ++t) qf[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
       }
 #pragma unroll
       for (int t = 0; t < KT; ++t) asm volatile("" : "+v"(qf[t]));
-      if (pend) {
-        store_partial<D>(acc, pend_inv, pend_lse, pend_row, g);
-        pend = false;
+      qn_unit = -1;
+      if (cc.u + 1 < units && cc.lt + ntiles - i > cc.tiles) {  // the share reaches unit u + 1
+#pragma unroll
+        for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u + 1) + 64 * t);
+        qn_unit = cc.u + 1;
       }
 #pragma unroll
       for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       m = -INFINITY;
       l = 0.f;
     }
-    // the unit starting two tiles ahead: its query rows
-    if (i + 2 < ntiles) {
-      cursor_next(a, sm, cq);
-      if (qn_unit < 0 && cq.lt == 0) {
-#pragma unroll
-        for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cq.u) + 64 * t);
-        qn_unit = cq.u;
+    compute_tile<D>(a, stage(i), qf, acc, m, l, cc.lt * TILE, cc.L, lane);
+    const bool end = cc.lt == cc.tiles - 1 || i == ntiles - 1;
+    if (end) {  // the segment ends: its partial
+      const float lt_sum = sum_over_groups(l);
+      const float inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
+      const float lse = m + log2f(lt_sum);
+      u32x2_t h[G::DB];
+      const float sc = make_partial<D>(acc, inv, h);
+      if (!prev_end) {
+        out_write<D, W>(out, h, lse, sc, wave, n, g);
+        lds_publish();
+      } else {
+        store_partial_rows<D>(a, h, lse, sc, ((int64_t)cc.u + share) * (16 * W) + wave * 16 + n, g);
       }
     }
-    compute_tile<D>(a, smem + (i & (S - 1)) * G::STAGE, qf, acc, m, l, cc.lt * TILE, cc.L, lane);
-    if (cc.lt == cc.tiles - 1 || i == ntiles - 1) {  // the segment ends
-      const float lt_sum = sum_over_groups(l);
-      pend = true;
-      pend_inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
-      pend_lse = m + log2f(lt_sum);
-      pend_row = ((int64_t)cc.u + share) * (16 * W) + wave * 16 + n;
-    }
+    prev_end = end;
     if (i + 1 < ntiles) cursor_next(a, sm, cc);
   }
-  if (pend) store_partial<D>(acc, pend_inv, pend_lse, pend_row, g);
+  block_sync();
 }
 
 // Merge each unit's partials (one per share its tiles fell to, in slots unit + w) and

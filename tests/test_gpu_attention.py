@@ -151,6 +151,25 @@ def test_paged_zero_length_gives_zeros(dev):
     assert (got[:t] == 0).all() and (got[2 * t:] == 0).all()
 
 
+def test_paged_large_batch(dev):
+    """More sequences than the streaming kernel stages in LDS (1024): the plan and the
+    lengths are then read with scalar loads. Short and empty sequences mixed."""
+    g = gen(17)
+    hq, hkv, d, t, page = 8, 2, 64, 16, 16
+    lens = torch.randint(0, 70, (1100,), generator=g)
+    lens[::97] = 0
+    b = len(lens)
+    bt, total = paged_layout(lens, page, g)
+    cache = torch.randn(total, hkv, page, 2 * d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
+    got = ops().block_attention_paged(
+        q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), t, 70, d ** -0.5
+    )
+    check_close(got, want)
+
+
 # ----------------------------------------------------------- token paged (a7)
 
 
