@@ -1,0 +1,84 @@
+"""The drop-in drafter (a10) on the GPU.
+
+- ``draft`` against the reference's own outputs on two tiny random-init drafters
+  (tests/golden/drafter_tiny.safetensors, written from flashmap/modeling_flashmap.py by
+  tests/golden/make_drafter_golden.py): logits within 2 % of the largest logit (max) and
+  0.5 % of the mean logit (mean), the -inf pattern of a state vocabulary exact, and the
+  greedy draft tokens
+  equal wherever the reference's top-2 margin exceeds twice the observed error.
+- ``spec_generate`` at temperature 0 is lossless: it returns the target's own greedy
+  decoding (the property flashmap/modeling_flashmap.py:525-528 states), on a tiny
+  random-init Qwen3 target.
+"""
+
+import json
+from pathlib import Path
+
+import pytest
+import torch
+
+from flashmap_amd import drafter as d
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "drafter_tiny.safetensors"
+
+
+def _load():
+    from safetensors import safe_open
+
+    with safe_open(str(GOLDEN), "pt") as f:
+        return json.loads(f.metadata()["cases"]), {k: f.get_tensor(k) for k in f.keys()}
+
+
+@pytest.mark.parametrize("name", ["gelu_full_vocab_1step", "swiglu_state_vocab_2step"])
+def test_draft_matches_reference(dev, name):
+    meta, t = _load()
+    case = meta[name]
+    model = d.FlashMapDraftModel(case["config"])
+    model.load_state_dict({k[len(name) + 7:]: v for k, v in t.items() if k.startswith(f"{name}/model/")})
+    model = model.to(dev, torch.bfloat16)
+    cfg = model.config
+    embed = torch.nn.Embedding(cfg.vocab_size, cfg.target_hidden_size, device=dev, dtype=torch.bfloat16)
+    head = torch.nn.Linear(cfg.target_hidden_size, cfg.vocab_size, bias=False, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        embed.weight.copy_(t[f"{name}/embed"])
+        head.weight.copy_(t[f"{name}/lm_head"])
+    cache = d.FlashMapCache(cfg, case["batch"], case["context"] + 1, device=dev, dtype=torch.bfloat16)
+    model.extend_context(cache, t[f"{name}/features"].to(dev))
+    got = model.draft(t[f"{name}/anchors"].to(dev), cache, embed, head, num_steps=case["num_steps"],
+                      noise=t[f"{name}/noise"].to(dev)).float().cpu()
+    want = t[f"{name}/logits"]
+    finite = torch.isfinite(want)
+    assert torch.equal(finite, torch.isfinite(got))
+    err = (got[finite] - want[finite]).abs()
+    scale = want[finite].abs()
+    assert err.max() <= 0.02 * scale.max(), f"max err {err.max():.4f} vs max |logit| {scale.max():.4f}"
+    assert err.mean() <= 0.005 * scale.mean(), f"mean err {err.mean():.5f} vs mean |logit| {scale.mean():.5f}"
+    top2 = want.masked_fill(~finite, float("-inf")).topk(2, dim=-1).values
+    clear = (top2[..., 0] - top2[..., 1]) > 2 * err.max()
+    print(f"{name}: max err {err.max():.4f} (max |logit| {scale.max():.4f}), mean err {err.mean():.5f} "
+          f"(mean |logit| {scale.mean():.4f}), clear-margin slots {clear.float().mean():.2f}", flush=True)
+    assert clear.float().mean() > 0.5
+    assert torch.equal(got.argmax(-1)[clear], want.argmax(-1)[clear])
+
+
+def test_spec_generate_is_lossless(dev):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    torch.manual_seed(7)
+    tcfg = Qwen3Config(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=3,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=32, max_position_embeddings=512)
+    target = Qwen3ForCausalLM(tcfg).to(dev).eval()
+    target.generation_config.eos_token_id = None
+    drafter = d.FlashMapDraftModel(dict(target_hidden_size=128, vocab_size=512, target_layer_ids=[0, 1],
+                                        hidden_size=128, num_hidden_layers=2, num_attention_heads=2,
+                                        intermediate_size=256, cond_dim=32, time_embed_dim=32)).to(dev, torch.bfloat16)
+    prompt = torch.randint(0, 512, (1, 11), device=dev)
+    n = 40
+    out = drafter.spec_generate(target, prompt, max_new_tokens=n, stop_token_ids=[])
+    want = target.generate(prompt, max_new_tokens=n, do_sample=False)
+    assert out.num_new_tokens == n
+    assert torch.equal(out.sequences, want[:, : prompt.shape[1] + n])
+    # the first new token comes from the prompt pass; every later pass commits 1 .. block + 1
+    assert sum(out.acceptance_lengths) + 1 >= n and all(1 <= a <= 17 for a in out.acceptance_lengths)
