@@ -53,6 +53,12 @@ SIGNATURES: dict[str, tuple] = {
         [*_Q, P, P, I64, I64, I64, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,
          *_PROLOGUE, *_SPLIT],
     ),
+    "fm_verify_workspace_bytes": (c_size_t, [I32, I32, I32, I32, I32, I32, I64, c_int]),
+    "fm_verify_attention": (
+        c_int,
+        [P, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, P, I64, I64, I64, I64, I64, P, P, I32,
+         P, P, I32, I32, I32, I32, I32, I32, F32, F32, F32, I32, P, c_size_t, P],
+    ),
     "fm_block_self_attention": (
         c_int, [P, P, I64, I32, I32, I32, P, P, *_ROPE, P, F32, F32, P]
     ),

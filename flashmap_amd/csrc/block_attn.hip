@@ -83,6 +83,10 @@ struct AttnArgs {
   uint32_t page_mask;           // page_size - 1 (power-of-two pages)
   uint32_t col_last, page_last; // table_width - 1, num_pages - 1
   int32_t page_size, page_shift;
+  // Token-paged (PAGED, page_size 1) only: csr != 0 reads sequence b's page ids at
+  // table[indptr[b] ..] and its length as indptr[b + 1] - indptr[b] (indptr passed in
+  // place of seqlens); ids are int32, or the low halves of int64 ids with id_shift 1.
+  int32_t csr, id_shift;
   int64_t k_s2, v_s2;           // position strides (elements)
   int64_t table_width, num_pages;
   const int32_t *table;
@@ -172,6 +176,17 @@ __device__ __forceinline__ void sload3(const int32_t *p, const int32_t *q, int32
   p0 = v[0];
   p1 = v[1];
 }
+// p[0], p[1], q[0] and q[1] in one round trip.
+__device__ __forceinline__ void sload2x2(const int32_t *p, const int32_t *q, int32_t &p0, int32_t &p1,
+                                         int32_t &q0, int32_t &q1) {
+  typedef __attribute__((ext_vector_type(2))) int32_t i32x2_t;
+  i32x2_t v, w;
+  asm volatile("s_load_dwordx2 %0, %2, 0x0\n\ts_load_dwordx2 %1, %3, 0x0\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(v), "=&s"(w)
+               : "s"(uniform_ptr(p)), "s"(uniform_ptr(q)));
+  p0 = v[0], p1 = v[1];
+  q0 = w[0], q1 = w[1];
+}
 
 // Per-sequence metadata (host-side helpers of the pack and combine kernels use plain
 // loads; the streaming kernel goes through SeqMeta).
@@ -192,6 +207,7 @@ __device__ __forceinline__ int64_t q_token_index(const AttnArgs &a, int b, int t
 // one tile at a time with compares only (no divisions on the per-tile path).
 struct Cursor {
   int b, h, rg, lt, tiles, L, u;
+  int64_t row;  // paged layouts: offset of sequence b's page ids in the table (ids)
 };
 
 // Sequences whose (tile prefix, length) the streaming kernel stages in LDS at its start,
@@ -216,21 +232,36 @@ struct SeqMeta {
     if (!var()) return (int64_t)b * a.uniform_tiles;
     return staged ? (int64_t)tab[b][0] : (int64_t)sload(plan + b);
   }
-  // tiles(b) = prefix(b + 1) - prefix(b) and the length of sequence b.
-  __device__ __forceinline__ void seq(const AttnArgs &a, int b, int &tiles, int &L) const {
+  // tiles(b) = prefix(b + 1) - prefix(b), the length of sequence b and the offset of
+  // its page ids. CSR: the second array is indptr, so the length is a difference.
+  __device__ __forceinline__ void seq(const AttnArgs &a, int b, int &tiles, int &L, int64_t &row) const {
     if (!var()) {
       tiles = a.uniform_tiles;
       L = a.uniform_len;
+      row = (int64_t)b * a.u.table_stride;
       return;
     }
     int32_t p0, p1, len;
-    if (staged) {
-      const i32x2_t e = tab[b];
-      p0 = e[0];
-      len = e[1];
-      p1 = tab[b + 1][0];
+    if (a.csr) {
+      int32_t s0, s1;
+      if (staged) {
+        const i32x2_t e = tab[b], f = tab[b + 1];
+        p0 = e[0], s0 = e[1], p1 = f[0], s1 = f[1];
+      } else {
+        sload2x2(plan + b, seqlens + b, p0, p1, s0, s1);
+      }
+      len = s1 - s0;
+      row = s0;
     } else {
-      sload3(plan + b, seqlens + b, p0, p1, len);
+      if (staged) {
+        const i32x2_t e = tab[b];
+        p0 = e[0];
+        len = e[1];
+        p1 = tab[b + 1][0];
+      } else {
+        sload3(plan + b, seqlens + b, p0, p1, len);
+      }
+      row = (int64_t)b * a.u.table_stride;
     }
     tiles = p1 - p0;
     L = len > 0 ? len : 0;
@@ -239,7 +270,7 @@ struct SeqMeta {
 
 template <bool VAR>
 __device__ __forceinline__ void cursor_load(const AttnArgs &a, const SeqMeta<VAR> &sm, Cursor &c) {
-  sm.seq(a, c.b, c.tiles, c.L);
+  sm.seq(a, c.b, c.tiles, c.L, c.row);
 }
 
 // Advance one tile; true when the next tile starts a new unit.
@@ -334,7 +365,7 @@ template <int LAYOUT, int D>
 __device__ __forceinline__ void issue_ids(const AttnArgs &a, const int32_t *__restrict__ table,
                                           const Cursor &c, char *stage, int lane) {
   using G = Geo<D>;
-  const int32_t *row = table + (int64_t)c.b * a.u.table_stride;
+  const int32_t *row = table + (c.row << a.id_shift);
   const int last = c.L - 1 > 0 ? c.L - 1 : 0;
   if (LAYOUT == PAGED16) {
     if (lane < 2) {
@@ -348,7 +379,8 @@ __device__ __forceinline__ void issue_ids(const AttnArgs &a, const int32_t *__re
     p = p < last ? p : last;
     int64_t col = a.page_size == 1 ? p : p / a.page_size;
     col = col < a.table_width ? col : a.table_width - 1;
-    __builtin_amdgcn_global_load_lds(row + col, (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(row + (col << a.id_shift), (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4,
+                                     0, 0);
   }
 }
 
@@ -768,7 +800,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens, (lds_i32x2_t *)seq_tab, false};
   if (sm.var() && a.batch <= SEQ_LDS) {  // uniform: every wavefront takes the barrier
     for (int j = threadIdx.x; j <= a.batch; j += blockDim.x) {
-      const int len = j < a.batch ? seqlens[j] : 0;
+      const int len = j < a.batch || a.csr ? seqlens[j] : 0;  // CSR: indptr[j]
       seq_tab[j] = i32x2_t{plan[j], len};
     }
     lds_publish();
@@ -794,7 +826,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     const int nr = (int)(share_start(sr + 1, total, a.num_shares) - share_start(sr, total, a.num_shares));
     nloop = nr > nloop ? nr : nloop;
   }
-  Cursor cc = Cursor{0, 0, 0, 0, 0, 0, 0};  // tile being computed (i)
+  Cursor cc = Cursor{0, 0, 0, 0, 0, 0, 0, 0};  // tile being computed (i)
   if (ntiles > 0) cc = cursor_at(a, sm, T0);
   auto stage = [&](int t) { return smem + (t % S) * G::STAGE; };
   // A segment ends at tile t when t is its unit's last or the share's last tile. Its
@@ -956,13 +988,67 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   block_sync();
 }
 
-// Merge each unit's partials (one per share its tiles fell to, in slots unit + w) and
-// write the bf16 output; units of empty sequences get zeros. One workgroup per 16-row
-// block, one thread per (row, 8 channels), so the unit and its sequence metadata are
-// uniform per workgroup.
+// Running log2-domain LSE merge of one thread's 8 channels of an output row: acc and den
+// are the segments' values and softmax masses, both relative to exp2(M).
+struct RowMerge {
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  float M = -INFINITY, den = 0.f;
+  // A segment whose values xs * x and mass d are relative to exp2(mseg) (finite).
+  __device__ __forceinline__ void add(float mseg, float xs, float d, const f32x4_t (&x)[2]) {
+    const float Mn = fmaxf(M, mseg);
+    const float fo = __builtin_amdgcn_exp2f(M - Mn), fn = __builtin_amdgcn_exp2f(mseg - Mn);
+    const float fx = fn * xs;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[j] = acc[j] * fo + x[j] * fx;
+    den = den * fo + d * fn;
+    M = Mn;
+  }
+  __device__ __forceinline__ void finish() {
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    acc[0] *= inv;
+    acc[1] *= inv;
+  }
+};
+
+// Adds the partials of row r of unit (b, ul) -- one per share its tiles fell to, in
+// slots unit + w -- each a normalized output with its LSE, values scaled by vs.
+template <int D>
+__device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, int b, int ul, int r, int c,
+                                               float vs, RowMerge &mg) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+  const int rows = a.nrb * 16;
+  const int64_t pre = tile_prefix(a, a.plan, b);
+  const int tiles_b = (int)(tile_prefix(a, a.plan, b + 1) - pre);
+  if (tiles_b <= 0) return;
+  const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
+  const int64_t nw = a.num_shares;
+  const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
+  const int64_t wa = share_of(U0, total, nw), wb = share_of(U0 + tiles_b - 1, total, nw);
+  // The loads of different segments are independent.
+#pragma unroll 4
+  for (int64_t w = wa; w <= wb; ++w) {
+    const int64_t row = (unit + w) * rows + r;
+    const f32x2_t ls = *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row);
+    const u32x4_t ow = load16(a.part_o + row * D + 8 * c);
+    if (ls[0] == -INFINITY) continue;
+    f32x4_t x[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      x[j] = f32x4_t{f16_lo(ow[2 * j]), f16_hi(ow[2 * j]), f16_lo(ow[2 * j + 1]), f16_hi(ow[2 * j + 1])};
+    mg.add(ls[0], ls[1] * vs, 1.f, x);
+  }
+}
+
+__device__ __forceinline__ void store_row8(uint16_t *dst, const f32x4_t (&acc)[2]) {
+  store16(dst, u32x4_t{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+                       pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])});
+}
+
+// Merge each unit's partials and write the bf16 output; units of empty sequences get
+// zeros. One workgroup per 16-row block, one thread per (row, 8 channels), so the unit
+// and its sequence metadata are uniform per workgroup.
 template <int D>
 __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
-  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
   constexpr int C = D / 8;  // 8-channel chunks per row
   const int rows = a.nrb * 16;
   const int64_t unit = blockIdx.x / a.nrb;
@@ -971,58 +1057,120 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
   const int b = (int)(unit / a.ups);
   const int ul = (int)(unit - (int64_t)b * a.ups);
   const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
-  const int64_t pre = tile_prefix(a, a.plan, b);
-  const int tiles_b = (int)(tile_prefix(a, a.plan, b + 1) - pre);
   const int qlen_b = q_rows_of(a, b);
   const int64_t first_tok = q_token_index(a, b, 0);
   const int R = rg * rows + r;
   const int gq = R / a.q_len, tq = R - gq * a.q_len;
   if (gq >= a.group || tq >= qlen_b) return;
-  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  if (tiles_b > 0) {
-    const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
-    const int64_t nw = a.num_shares;
-    const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
-    const int64_t wa = share_of(U0, total, nw), wb = share_of(U0 + tiles_b - 1, total, nw);
-    // Running LSE merge; the loads of different segments are independent.
-    float M = -INFINITY, den = 0.f;
-#pragma unroll 4
-    for (int64_t w = wa; w <= wb; ++w) {
-      const int64_t row = (unit + w) * rows + r;
-      const f32x2_t ls = *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row);
-      const u32x4_t ow = load16(a.part_o + row * D + 8 * c);
-      if (ls[0] == -INFINITY) continue;
-      const float Mn = fmaxf(M, ls[0]);
-      const float fo = __builtin_amdgcn_exp2f(M - Mn), ew = __builtin_amdgcn_exp2f(ls[0] - Mn);
-      const float fw = ew * ls[1];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[j] = acc[j] * fo + f32x4_t{f16_lo(ow[2 * j]), f16_hi(ow[2 * j]), f16_lo(ow[2 * j + 1]),
-                                       f16_hi(ow[2 * j + 1])} * fw;
-      den = den * fo + ew;
-      M = Mn;
-    }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    acc[0] *= inv;
-    acc[1] *= inv;
-  }
+  RowMerge mg;
+  merge_partials<D>(a, unit, b, ul, r, c, 1.f, mg);
+  mg.finish();
   const int64_t head = (int64_t)h * a.group + gq;
-  uint16_t *dst = a.o +
-                  (a.cu_q ? (first_tok + tq) * a.o_st : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
-                  head * a.o_sh + 8 * c;
-  store16(dst, u32x4_t{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
-                       pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])});
+  store_row8(a.o + (a.cu_q ? (first_tok + tq) * a.o_st : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
+                 head * a.o_sh + 8 * c,
+             mg.acc);
 }
 
-// plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(seqlens[b], 0) / TILE).
+// The verify tokens' own keys and values and the mask among them (target verification:
+// every request has q_len tokens that see its whole context and, among themselves,
+// what the mask allows).
+struct VerifyArgs {
+  const uint16_t *k, *v;  // (batch * q_len, kv heads, D): token b * q_len + j
+  int64_t k_st, k_sh, v_st, v_sh;
+  const uint8_t *mask;         // mode 1 / 2; nonzero = visible
+  const int64_t *mask_indptr;  // mode 1: start of request b's mask rows
+  int32_t mode;                // 0 causal, 1 rows of context + q_len entries, 2 q_len x q_len blocks
+  float scale_log2;            // softmax_scale * log2(e) of the tokens' scores
+  float v_scale;               // scale of the context's values
+};
+
+// Sum over the C lanes that hold one row (consecutive lanes, C a power of two <= 16).
+template <int C>
+__device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+  for (int o = C / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// The combine of a verify call: each row's attention to its request's verify tokens
+// (at most q_len keys, masked), merged with the context partials of the streaming
+// kernel. Same thread layout as attn_combine_kernel; every lane stays active to the
+// end (the row sums cross lanes), rows past the group store nothing.
+template <int D>
+__global__ __launch_bounds__(2 * D) void verify_combine_kernel(const AttnArgs a, const VerifyArgs v) {
+  constexpr int C = D / 8;
+  const int rows = a.nrb * 16;
+  const int64_t unit = blockIdx.x / a.nrb;
+  const int r = (int)(blockIdx.x - unit * a.nrb) * 16 + (int)threadIdx.x / C;
+  const int c = (int)threadIdx.x % C;
+  const int b = (int)(unit / a.ups);
+  const int ul = (int)(unit - (int64_t)b * a.ups);
+  const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
+  const int L = a.q_len;
+  const int R = rg * rows + r;
+  const int gq = R / L, tq = R - gq * L;
+  const bool valid = gq < a.group;
+  RowMerge mg;
+  merge_partials<D>(a, unit, b, ul, r, c, v.v_scale, mg);
+  // The row's query (packed rows: zero past the group).
+  const u32x4_t qw = load16(a.qp + (unit * rows + r) * D + 8 * c);
+  float q[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) q[2 * j] = bf16_lo(qw[j]), q[2 * j + 1] = bf16_hi(qw[j]);
+  const int64_t tok0 = (int64_t)b * L;
+  const uint16_t *kb = v.k + h * v.k_sh + 8 * c;
+  const uint16_t *vb = v.v + h * v.v_sh + 8 * c;
+  int64_t mrow = 0;  // mask entry of (row tq, token 0)
+  if (v.mode == 1) {
+    const int ctx = a.seqlens[b + 1] - a.seqlens[b];  // CSR: indptr
+    mrow = v.mask_indptr[b] + (int64_t)tq * (ctx + L) + ctx;
+  } else if (v.mode == 2) {
+    mrow = (tok0 + tq) * L;
+  }
+  auto score = [&](int j) {
+    const u32x4_t kw = load16(kb + (tok0 + j) * v.k_st);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s += q[2 * i] * bf16_lo(kw[i]) + q[2 * i + 1] * bf16_hi(kw[i]);
+    return row_sum<C>(s) * v.scale_log2;
+  };
+  auto visible = [&](int j) { return v.mode == 0 ? j <= tq : v.mask[mrow + j] != 0; };
+  float mt = -INFINITY;
+  for (int j = 0; j < L; ++j) {
+    const float s = score(j);
+    if (visible(j)) mt = fmaxf(mt, s);
+  }
+  // (A row with no visible token has mt = -inf and p = 0 throughout; no branch, so the
+  // row sums never run under divergence.)
+  f32x4_t at[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  float lt = 0.f;
+  for (int j = 0; j < L; ++j) {
+    const float s = score(j);
+    const float p = visible(j) ? __builtin_amdgcn_exp2f(s - mt) : 0.f;
+    lt += p;
+    const float pb = round_bf16(p);  // P . V in bf16 operands
+    const u32x4_t vw = load16(vb + (tok0 + j) * v.v_st);
+    at[0] += f32x4_t{bf16_lo(vw[0]), bf16_hi(vw[0]), bf16_lo(vw[1]), bf16_hi(vw[1])} * pb;
+    at[1] += f32x4_t{bf16_lo(vw[2]), bf16_hi(vw[2]), bf16_lo(vw[3]), bf16_hi(vw[3])} * pb;
+  }
+  if (lt > 0.f) mg.add(mt, 1.f, lt, at);
+  mg.finish();
+  if (!valid) return;
+  const int64_t head = (int64_t)h * a.group + gq;
+  store_row8(a.o + (int64_t)b * a.o_sb + (int64_t)tq * a.o_st + head * a.o_sh + 8 * c, mg.acc);
+}
+
+// plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(L_b, 0) / TILE), L_b = seqlens[b], or
+// seqlens[b + 1] - seqlens[b] when seqlens is a CSR indptr (csr != 0).
 __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restrict__ seqlens,
-                                                         int32_t batch, int32_t *__restrict__ plan) {
+                                                         int32_t batch, int32_t *__restrict__ plan,
+                                                         int32_t csr) {
   __shared__ int32_t buf[1024];
   int32_t carry = 0;
   if (threadIdx.x == 0) plan[0] = 0;
   for (int base = 0; base < batch; base += 1024) {
     const int i = base + threadIdx.x;
-    int32_t L = i < batch ? seqlens[i] : 0;
+    int32_t L = i < batch ? (csr ? seqlens[i + 1] - seqlens[i] : seqlens[i]) : 0;
     L = L > 0 ? L : 0;
     buf[threadIdx.x] = (L + TILE - 1) / TILE;
     __syncthreads();
@@ -1168,7 +1316,8 @@ struct CommonIn {
   hipStream_t stream;
 };
 
-static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
+// vf: a verify call (its combine also attends to the verify tokens).
+static int run_attention(const CommonIn &c, int layout, AttnArgs a, const VerifyArgs *vf = nullptr) {
   FM_REQUIRE(c.batch >= 0 && c.q_len >= 0 && c.hq > 0 && c.hkv > 0, "bad sizes");
   if (c.batch == 0 || c.q_len == 0) return FM_OK;
   if (c.d != 64 && c.d != 128) return fail(FM_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", c.d);
@@ -1232,7 +1381,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
   if (a.seqlens != nullptr) {
     if (need_plan) {
       int32_t *plan = (int32_t *)(ws + sz.plan_off);
-      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, plan);
+      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, plan, a.csr);
       FM_CHECK_HIP(hipGetLastError());
       a.plan = plan;
     } else {
@@ -1259,10 +1408,16 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a) {
   // One workgroup of 2 D threads per 16-row block.
   const int64_t cblocks = units * sz.rp.nrb;
   FM_REQUIRE(cblocks < (1ll << 31), "too many units");
-  if (c.d == 128)
+  if (vf != nullptr) {
+    if (c.d == 128)
+      verify_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a, *vf);
+    else
+      verify_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(128), 0, c.stream>>>(a, *vf);
+  } else if (c.d == 128) {
     attn_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
-  else
+  } else {
     attn_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(128), 0, c.stream>>>(a);
+  }
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
@@ -1278,7 +1433,7 @@ extern "C" size_t fm_attn_plan_bytes(int32_t batch) {
 extern "C" int fm_attn_plan(const int32_t *seqlens, int32_t batch, int32_t *plan, void *stream) {
   FM_REQUIRE(batch >= 0, "bad batch");
   FM_REQUIRE(plan != nullptr && (batch == 0 || seqlens != nullptr), "NULL pointer");
-  attn_plan_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(seqlens, batch, plan);
+  attn_plan_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(seqlens, batch, plan, 0);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
@@ -1405,4 +1560,76 @@ extern "C" int fm_block_attn_token_paged(
   a.page_shift = 0;
   a.seqlens = cache_seqlens;
   return run_attention(c, PAGED, a);
+}
+
+// Context length a verify call plans its grid for: the hint, else the pool size (a
+// request cannot hold more distinct pool rows).
+static int32_t verify_max_context(int32_t max_context, int64_t pool_size) {
+  if (max_context > 0) return max_context;
+  return (int32_t)(pool_size < 0x7fffffffll ? pool_size : 0x7fffffffll);
+}
+
+extern "C" size_t fm_verify_workspace_bytes(int32_t batch, int32_t verify_len, int32_t num_q_heads,
+                                            int32_t num_kv_heads, int32_t head_dim, int32_t max_context,
+                                            int64_t pool_size, int device) {
+  if (batch <= 0 || verify_len <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      (head_dim != 64 && head_dim != 128))
+    return 256;
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess) return 0;
+  if (device != prev && hipSetDevice(device) != hipSuccess) return 0;
+  Sizing sz;
+  const int rc = sizing(PAGED, batch, verify_len, num_q_heads, num_kv_heads, head_dim,
+                        verify_max_context(max_context, pool_size), true, &sz);
+  if (device != prev) hipSetDevice(prev);
+  return rc == FM_OK ? sz.bytes : 0;
+}
+
+extern "C" int fm_verify_attention(
+    const void *q, int64_t q_stride_token, int64_t q_stride_head, const void *k_ext,
+    int64_t k_ext_stride_token, int64_t k_ext_stride_head, const void *v_ext, int64_t v_ext_stride_token,
+    int64_t v_ext_stride_head, void *out, int64_t out_stride_token, int64_t out_stride_head,
+    const void *key_buffer, const void *value_buffer, int64_t pool_size, int64_t k_stride_slot,
+    int64_t k_stride_head, int64_t v_stride_slot, int64_t v_stride_head, const int32_t *kv_indptr,
+    const void *kv_indices, int32_t kv_index_bytes, const uint8_t *custom_mask, const int64_t *mask_indptr,
+    int32_t mask_mode, int32_t batch, int32_t verify_len, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, float sm_scale, float k_scale, float v_scale, int32_t max_context,
+    void *workspace, size_t workspace_bytes, void *stream) {
+  FM_REQUIRE(batch >= 0 && verify_len >= 0, "bad sizes");
+  if (batch == 0 || verify_len == 0) return FM_OK;
+  FM_REQUIRE(key_buffer && value_buffer && kv_indptr && kv_indices, "NULL pool/indptr/indices");
+  FM_REQUIRE(k_ext && v_ext, "NULL verify keys/values");
+  FM_REQUIRE(pool_size > 0, "bad pool size");
+  FM_REQUIRE(kv_index_bytes == 4 || kv_index_bytes == 8, "kv_indices must be int32 or int64");
+  FM_REQUIRE(mask_mode >= 0 && mask_mode <= 2, "mask_mode %d (0 causal, 1 full rows, 2 verify blocks)",
+             mask_mode);
+  FM_REQUIRE(mask_mode == 0 || custom_mask != nullptr, "the mask mode needs custom_mask");
+  FM_REQUIRE(mask_mode != 1 || mask_indptr != nullptr, "full-row masks need mask_indptr");
+  FM_REQUIRE(al16(k_ext) && al16(v_ext), "verify keys/values must be 16-byte aligned");
+  FM_REQUIRE(k_ext_stride_token % 8 == 0 && k_ext_stride_head % 8 == 0 && v_ext_stride_token % 8 == 0 &&
+                 v_ext_stride_head % 8 == 0,
+             "verify key/value strides must be multiples of 8 elements");
+  const int64_t q_sb = (int64_t)verify_len * q_stride_token, o_sb = (int64_t)verify_len * out_stride_token;
+  CommonIn c{q, q_sb, q_stride_token, q_stride_head, out, o_sb, out_stride_token, out_stride_head,
+             nullptr, batch, verify_len, verify_max_context(max_context, pool_size), num_q_heads,
+             num_kv_heads, head_dim, sm_scale * k_scale, nullptr, nullptr, nullptr, 0, 0, 0, nullptr,
+             0.f, nullptr, workspace, workspace_bytes, (hipStream_t)stream};
+  AttnArgs a{};
+  a.u.k = (const uint16_t *)key_buffer;
+  a.u.v = (const uint16_t *)value_buffer;
+  a.u.k_s0 = k_stride_slot, a.u.k_s1 = k_stride_head, a.k_s2 = 0;
+  a.u.v_s0 = v_stride_slot, a.u.v_s1 = v_stride_head, a.v_s2 = 0;
+  a.table = (const int32_t *)kv_indices;
+  a.u.table_stride = 0;
+  a.table_width = 1ll << 40;  // CSR rows are bounded by indptr, not by a table width
+  a.num_pages = pool_size;
+  a.page_size = 1;
+  a.page_shift = 0;
+  a.csr = 1;
+  a.id_shift = kv_index_bytes == 8 ? 1 : 0;
+  a.seqlens = kv_indptr;
+  VerifyArgs vf{(const uint16_t *)k_ext, (const uint16_t *)v_ext, k_ext_stride_token, k_ext_stride_head,
+                v_ext_stride_token, v_ext_stride_head, custom_mask, mask_indptr, mask_mode,
+                sm_scale * 1.4426950408889634f, v_scale};
+  return run_attention(c, PAGED, a, &vf);
 }

@@ -28,6 +28,8 @@ __all__ = [
     "rope_from_cat",
     "rope_from_split",
     "rope_from_table",
+    "verify_attention",
+    "verify_workspace_bytes",
     "workspace_for",
     "write_context_kv",
     "write_context_kv_pool",
@@ -363,6 +365,115 @@ def block_attention_token_paged(
         hq, hkv, d, float(scale),
         *(prologue.args() if prologue else _NO_PROLOGUE),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
+# ------------------------------------------------------------------ verify attention
+
+_VERIFY_WS_BYTES: dict[tuple, int] = {}
+
+
+def verify_workspace_bytes(batch: int, verify_len: int, hq: int, hkv: int, head_dim: int, max_context: int,
+                           pool_size: int, device: torch.device) -> int:
+    """Workspace bytes of a verify call of these sizes (fm_verify_workspace_bytes)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (batch, verify_len, hq, hkv, head_dim, max_context, pool_size, index)
+    nbytes = _VERIFY_WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = int(_native.lib().fm_verify_workspace_bytes(batch, verify_len, hq, hkv, head_dim, max_context,
+                                                             pool_size, index))
+        if nbytes == 0:
+            raise RuntimeError(f"fm_verify_workspace_bytes failed: {_native.last_error()}")
+        _VERIFY_WS_BYTES[key] = nbytes
+    return nbytes
+
+
+def _verify_rows(x: torch.Tensor, name: str) -> bool:
+    """Whether ``x`` is bf16 with unit channel stride, 16-byte aligned, other strides
+    multiples of 8 elements: the layout the verify kernels read in place."""
+    return (x.dtype == torch.bfloat16 and x.stride(-1) == 1 and x.data_ptr() % 16 == 0
+            and all(st % 8 == 0 for st in x.stride()[:-1]))
+
+
+def verify_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    custom_mask: torch.Tensor | None = None,
+    mask_indptr: torch.Tensor | None = None,
+    qlen_mask: bool = False,
+    sm_scale: float | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    out: torch.Tensor | None = None,
+    max_context: int | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Target verify attention (flashmap/sglang/verify_attention.py:35-233, 360-474):
+    ``q (bs * L, Hq, D)`` -- L verify tokens per request -- attends to request b's
+    context, pool rows ``kv_indices[kv_indptr[b]:kv_indptr[b + 1]]`` of
+    ``key_buffer/value_buffer (pool, Hkv, D)``, and to the verify tokens' own keys and
+    values ``k, v (bs * L, Hkv, D)`` causally (``custom_mask`` None), under sglang's
+    custom mask (rows of context + L entries at ``mask_indptr[b]``, the last L of which
+    apply) or, with ``qlen_mask``, under each request's L x L block at ``b * L * L``.
+    Context scores are scaled by ``sm_scale * k_scale``, context values by
+    ``v_scale``. Returns ``out (bs * L, Hq, D)`` bf16. ``workspace`` (uint8, at least
+    :func:`verify_workspace_bytes`) defaults to the device's persistent one."""
+    _check_cuda(q, k, v, key_buffer, value_buffer, kv_indptr, kv_indices, custom_mask, mask_indptr)
+    bs = kv_indptr.shape[0] - 1
+    tokens, hq, d = q.shape
+    pool, hkv, _ = key_buffer.shape
+    if bs < 1 or tokens == 0:
+        return torch.empty_like(q) if out is None else out
+    if tokens % bs:
+        raise ValueError(f"q holds {tokens} tokens, not a multiple of the {bs} requests")
+    length = tokens // bs
+    q = _bf16_rows(q, "q")
+    k = _bf16_rows(k.view(-1, hkv, d), "k")
+    v = _bf16_rows(v.view(-1, hkv, d), "v")
+    key_buffer, value_buffer = _bf16_rows(key_buffer, "key_buffer"), _bf16_rows(value_buffer, "value_buffer")
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    elif not _verify_rows(out, "out"):
+        raise ValueError("out must be bf16 with unit channel stride, 16-byte aligned, strides multiples of 8")
+    indptr = _i32(kv_indptr)
+    if kv_indices.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"kv_indices must be int32 or int64, got {kv_indices.dtype}")
+    indices = kv_indices.contiguous()
+    mode, mask, mptr = 0, None, None
+    if custom_mask is not None:
+        if custom_mask.element_size() != 1:
+            raise TypeError(f"custom_mask must hold one byte per entry (bool/uint8), got {custom_mask.dtype}")
+        mask = custom_mask.contiguous()
+        if qlen_mask:
+            mode = 2
+        else:
+            if mask_indptr is None:
+                raise ValueError("a custom mask in sglang's layout needs mask_indptr")
+            mode, mptr = 1, _i64(mask_indptr)
+    scale = d ** -0.5 if sm_scale is None else float(sm_scale)
+    ctx = 0 if max_context is None else int(max_context)
+    nbytes = verify_workspace_bytes(bs, length, hq, hkv, d, ctx, pool, q.device)
+    if workspace is None:
+        index = q.device.index if q.device.index is not None else torch.cuda.current_device()
+        workspace = _WORKSPACES.get(torch.device("cuda", index), nbytes)
+    elif workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, need {nbytes}")
+    call(
+        "fm_verify_attention",
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+        key_buffer.data_ptr(), value_buffer.data_ptr(), pool,
+        key_buffer.stride(0), key_buffer.stride(1), value_buffer.stride(0), value_buffer.stride(1),
+        indptr.data_ptr(), indices.data_ptr(), indices.element_size(),
+        _ptr(mask), _ptr(mptr), mode, bs, length, hq, hkv, d,
+        scale, float(k_scale), float(v_scale), ctx,
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(q),
     )
     return out
 

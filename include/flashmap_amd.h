@@ -165,6 +165,44 @@ int fm_block_attn_token_paged(
     size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------------
+ * Target verify attention: the step after the draft. Each request b has verify_len (L)
+ * tokens -- the draft and its root, as a chain or a tree -- that attend to the
+ * request's cached context and, among themselves, to what the mask allows. Replaces
+ * SplitKVVerify (flashmap/sglang/verify_attention.py:251-474; its kernels :35-233,
+ * installed as the target's verify_splitkv_fwd by flashmap/sglang/tree_worker.py:79-99),
+ * taking sglang's extend_attention_fwd arguments as plain pointers:
+ *   q, out: (batch * L, num_q_heads, head_dim), row of token b * L + t;
+ *   k_ext, v_ext: the verify tokens' own keys/values (batch * L, num_kv_heads, head_dim);
+ *   key_buffer, value_buffer: the pool (pool_size, num_kv_heads, head_dim);
+ *   context of request b: pool rows kv_indices[kv_indptr[b] .. kv_indptr[b + 1]),
+ *     kv_indices int32 or int64 (kv_index_bytes 4 / 8), kv_indptr int32 (batch + 1);
+ *   mask_mode 0: causal among the verify tokens (token t sees tokens 0..t);
+ *     1: sglang's custom mask, request b's rows at custom_mask[mask_indptr[b]], each
+ *        context + L bytes of which the last L apply (the context is always visible);
+ *     2: EAGLE's QLEN_ONLY layout, request b's L x L block at custom_mask[b * L * L];
+ *     custom_mask bytes: nonzero = visible; mask_indptr int64 (batch + 1).
+ * Context scores are scaled by sm_scale * k_scale and context values by v_scale; the
+ * verify tokens' by sm_scale alone. A row that sees nothing gets zeros. Query heads
+ * h * G .. h * G + G - 1 (G = num_q_heads / num_kv_heads) read KV head h.
+ * max_context (> 0) bounds every request's context for grid planning; <= 0 uses
+ * pool_size. Only sizes are read on the host. head_dim in {64, 128}, bf16.
+ */
+size_t fm_verify_workspace_bytes(int32_t batch, int32_t verify_len, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t max_context,
+                                 int64_t pool_size, int device);
+int fm_verify_attention(
+    const void *q, int64_t q_stride_token, int64_t q_stride_head, const void *k_ext,
+    int64_t k_ext_stride_token, int64_t k_ext_stride_head, const void *v_ext,
+    int64_t v_ext_stride_token, int64_t v_ext_stride_head, void *out, int64_t out_stride_token,
+    int64_t out_stride_head, const void *key_buffer, const void *value_buffer, int64_t pool_size,
+    int64_t k_stride_slot, int64_t k_stride_head, int64_t v_stride_slot, int64_t v_stride_head,
+    const int32_t *kv_indptr, const void *kv_indices, int32_t kv_index_bytes,
+    const uint8_t *custom_mask, const int64_t *mask_indptr, int32_t mask_mode, int32_t batch,
+    int32_t verify_len, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float sm_scale, float k_scale, float v_scale, int32_t max_context, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------------
  * a8  Block self-attention with fused q/k RMSNorm + RoPE: qkv (blocks, block_size,
  * 3, heads, head_dim) bf16 contiguous -> out (blocks, block_size, heads, head_dim)
  * bf16 contiguous (the same bytes as vLLM's (blocks * block_size, heads * head_dim)).

@@ -219,6 +219,73 @@ def block_attention_token_paged(query, key_buffer, value_buffer, cache_seqlens, 
     return out
 
 
+# --------------------------------------------------------------- verify attention
+
+
+def verify_visibility(b: int, length: int, context: int, custom_mask=None, mask_indptr=None,
+                      qlen_mask: bool = False) -> torch.Tensor:
+    """``(L, L)`` bool: verify token t of request b sees verify token j. No mask: causal
+    (j <= t). sglang's layout: request b's rows start at ``mask_indptr[b]``, each
+    ``context + L`` entries of which the last L apply (the context columns are never
+    read: the context is always visible). QLEN_ONLY: request b's ``L x L`` block at
+    ``b * L * L`` (flashmap/sglang/verify_attention.py:143-164).
+    Pinned by: causal == the lower-triangular mask in both layouts, context columns
+    ignored (test_oracle_verify)."""
+    if custom_mask is None:
+        return torch.ones(length, length, dtype=torch.bool).tril()
+    m = torch.as_tensor(custom_mask).reshape(-1)
+    if qlen_mask:
+        return m[b * length * length:(b + 1) * length * length].reshape(length, length) != 0
+    start = int(mask_indptr[b])
+    rows = m[start:start + length * (context + length)].reshape(length, context + length)
+    return rows[:, context:] != 0
+
+
+def verify_attention(q, k_ext, v_ext, key_buffer, value_buffer, kv_indptr, kv_indices, custom_mask=None,
+                     mask_indptr=None, qlen_mask=False, sm_scale=None, k_scale=1.0, v_scale=1.0):
+    """Target verify attention, SplitKVVerify (flashmap/sglang/verify_attention.py:35-233,
+    360-474): ``q (bs * L, Hq, D)`` row ``b * L + t`` (query head hq, KV head
+    ``hq // (Hq / Hkv)``) attends to request b's context, pool rows
+    ``kv_indices[kv_indptr[b]:kv_indptr[b + 1]]`` of ``key_buffer/value_buffer (pool,
+    Hkv, D)`` with scores scaled by ``sm_scale * k_scale`` and values by ``v_scale``, and
+    to the verify tokens j of ``k_ext/v_ext (bs * L, Hkv, D)`` that
+    :func:`verify_visibility` allows, scores scaled by ``sm_scale``; one softmax over
+    both (the reference splits it into partials merged by LSE, which is the same
+    function). A row that sees nothing is zero. Returns float32 (bs * L, Hq, D).
+    Pinned by: float64 brute force per row; == lse_merge of the context and verify
+    partials (the reference's split form); L = 1 causal == :func:`attention` onto the
+    context plus the token; k_scale / v_scale == pre-scaled pool; GQA == MHA on repeated
+    KV (test_oracle_verify)."""
+    bs = len(kv_indptr) - 1
+    tokens, hq, d = q.shape
+    length = tokens // bs
+    hkv = key_buffer.shape[1]
+    g = hq // hkv
+    scale = d ** -0.5 if sm_scale is None else sm_scale
+    out = torch.zeros((tokens, hq, v_ext.shape[-1]))
+    for b in range(bs):
+        lo, hi = int(kv_indptr[b]), int(kv_indptr[b + 1])
+        n = max(hi - lo, 0)
+        rows = torch.as_tensor(np.asarray(kv_indices)[lo:lo + n]).long()
+        kp, vp = key_buffer[rows].float(), value_buffer[rows].float()  # (n, Hkv, D)
+        ke, ve = k_ext[b * length:(b + 1) * length].float(), v_ext[b * length:(b + 1) * length].float()
+        vis = verify_visibility(b, length, n, custom_mask, mask_indptr, qlen_mask)
+        qb = q[b * length:(b + 1) * length].float()  # (L, Hq, D)
+        for h in range(hq):
+            kh = h // g
+            sp = (qb[:, h] @ kp[:, kh].T) * (scale * k_scale)  # (L, n)
+            se = (qb[:, h] @ ke[:, kh].T) * scale  # (L, L)
+            se = se.masked_fill(~vis, -math.inf)
+            s = torch.cat([sp, se], dim=1)
+            m = s.max(dim=1, keepdim=True).values
+            m = torch.where(torch.isinf(m), torch.zeros_like(m), m)
+            p = torch.exp(s - m)
+            den = p.sum(dim=1, keepdim=True)
+            o = p[:, :n] @ vp[:, kh] * v_scale + p[:, n:] @ ve[:, kh]
+            out[b * length:(b + 1) * length, h] = o / torch.where(den > 0, den, torch.ones_like(den))
+    return out
+
+
 # -------------------------------------------------------------- self-attention (a8)
 
 

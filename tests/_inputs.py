@@ -75,3 +75,52 @@ def check_close(got: torch.Tensor, want: torch.Tensor, max_abs=MAX_ABS, mean_abs
     assert err.max().item() <= max_abs, f"max-abs {err.max().item():.3e} > {max_abs}"
     assert err.mean().item() <= mean_abs, f"mean-abs {err.mean().item():.3e} > {mean_abs}"
     return err
+
+
+def tree_visibility(length: int, g: torch.Generator) -> torch.Tensor:
+    """``(L, L)`` bool visibility of a random draft tree: node 0 is the root, node j's
+    parent is drawn from nodes 0..j-1, and a node sees itself and its ancestors."""
+    parent = [-1] + [int(torch.randint(0, j, (1,), generator=g)) for j in range(1, length)]
+    vis = torch.zeros(length, length, dtype=torch.bool)
+    for j in range(length):
+        a = j
+        while a >= 0:
+            vis[j, a] = True
+            a = parent[a]
+    return vis
+
+
+def verify_case(bs, length, hq, hkv, d, contexts, mask="causal", index_dtype=torch.int32, seed=0,
+                pool_slack=37, dtype=torch.bfloat16):
+    """Seeded inputs of a verify call in sglang's extend_attention_fwd layout:
+    q ``(bs * L, Hq, D)``, the verify tokens' k/v ``(bs * L, Hkv, D)``, a pool
+    ``(pool, Hkv, D)`` whose rows hold every request's context at randomly permuted slots
+    (plus unused rows), ``kv_indptr``/``kv_indices`` and, for ``mask`` "rows" (sglang's
+    layout, the context columns filled with junk the kernels must not read) or "qlen"
+    (L x L blocks), per-request random tree masks."""
+    g = gen(seed)
+    contexts = [int(c) for c in contexts]
+    total = sum(contexts)
+    pool = total + pool_slack
+    q = torch.randn(bs * length, hq, d, generator=g).to(dtype)
+    k = torch.randn(bs * length, hkv, d, generator=g).to(dtype)
+    v = torch.randn(bs * length, hkv, d, generator=g).to(dtype)
+    key_buffer = torch.randn(pool, hkv, d, generator=g).to(dtype)
+    value_buffer = torch.randn(pool, hkv, d, generator=g).to(dtype)
+    kv_indptr = torch.zeros(bs + 1, dtype=torch.int32)
+    kv_indptr[1:] = torch.cumsum(torch.tensor(contexts, dtype=torch.int64), 0).to(torch.int32)
+    kv_indices = torch.randperm(pool, generator=g)[:total].to(index_dtype)
+    case = dict(q=q, k=k, v=v, key_buffer=key_buffer, value_buffer=value_buffer, kv_indptr=kv_indptr,
+                kv_indices=kv_indices, custom_mask=None, mask_indptr=None, qlen_mask=False)
+    if mask == "rows":
+        rows, starts = [], [0]
+        for b in range(bs):
+            junk = torch.randint(0, 2, (length, contexts[b]), generator=g).bool()
+            rows.append(torch.cat([junk, tree_visibility(length, g)], dim=1).reshape(-1))
+            starts.append(starts[-1] + length * (contexts[b] + length))
+        case["custom_mask"] = torch.cat(rows)
+        case["mask_indptr"] = torch.tensor(starts, dtype=torch.int64)
+    elif mask == "qlen":
+        case["custom_mask"] = torch.cat([tree_visibility(length, g).reshape(-1) for _ in range(bs)])
+        case["qlen_mask"] = True
+    return case

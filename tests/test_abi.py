@@ -107,3 +107,36 @@ def test_wrappers_refuse_cpu_tensors():
     table = torch.zeros(16, 64, 2)
     with pytest.raises(ValueError, match="GPU"):
         ops.rms_norm_rope(x, torch.ones(128), ops.rope_from_table(table), None, 1e-6)
+
+
+def test_verify_argument_errors(lib):
+    from flashmap_amd import _native as n
+
+    x = ctypes.c_void_p(16)
+    f = ctypes.c_float
+    qkvo = [x, 4096, 128, x, 1024, 128, x, 1024, 128, x, 4096, 128]
+    pool = [x, x, 100, 1024, 128, 1024, 128]
+    tail = [4, 17, 32, 8, 128, f(0.088), f(1.0), f(1.0), 0, None, 0, None]
+    # zero requests or tokens: nothing to do
+    assert lib.fm_verify_attention(*qkvo, *pool, x, x, 4, None, None, 0, 0, *tail[1:]) == n.FM_OK
+    # NULL indptr
+    rc = lib.fm_verify_attention(*qkvo, *pool, None, x, 4, None, None, 0, *tail)
+    assert rc == n.FM_ERR_INVALID and "NULL" in _err(lib)
+    # index width
+    rc = lib.fm_verify_attention(*qkvo, *pool, x, x, 2, None, None, 0, *tail)
+    assert rc == n.FM_ERR_INVALID and "int32 or int64" in _err(lib)
+    # mask modes and their arrays
+    rc = lib.fm_verify_attention(*qkvo, *pool, x, x, 4, None, None, 3, *tail)
+    assert rc == n.FM_ERR_INVALID and "mask_mode 3" in _err(lib)
+    rc = lib.fm_verify_attention(*qkvo, *pool, x, x, 4, None, None, 2, *tail)
+    assert rc == n.FM_ERR_INVALID and "custom_mask" in _err(lib)
+    rc = lib.fm_verify_attention(*qkvo, *pool, x, x, 4, x, None, 1, *tail)
+    assert rc == n.FM_ERR_INVALID and "mask_indptr" in _err(lib)
+    # verify-token strides
+    bad = list(qkvo)
+    bad[4] = 1020
+    rc = lib.fm_verify_attention(*bad, *pool, x, x, 4, None, None, 0, *tail)
+    assert rc == n.FM_ERR_INVALID and "multiples of 8" in _err(lib)
+    # invalid shapes answer the workspace query with a minimal size
+    assert lib.fm_verify_workspace_bytes(4, 17, 30, 8, 128, 0, 1000, 0) == 256
+    assert lib.fm_verify_workspace_bytes(4, 17, 32, 8, 96, 0, 1000, 0) == 256
