@@ -152,12 +152,127 @@ def cpu_baseline(inp, budget_s: float = 12.0) -> dict:
     }
 
 
+# Target verify attention (SplitKVVerify's call): name -> (batch, hq, hkv, head_dim,
+# verify tokens, ctx lo, ctx hi, mask). Contexts as the drafter workloads draw them,
+# held in an SGLang token pool at randomly permuted slots.
+VERIFY_WORKLOADS = {
+    "verify-qwen3-8b-chain-b64": (64, 32, 8, 128, 17, 256, 8192, "causal"),
+    "verify-qwen3-8b-tree-b64": (64, 32, 8, 128, 17, 256, 8192, "qlen"),
+}
+
+
+def run_verify(args, dev) -> dict:
+    """One call = fm_verify_attention over the batch: plan, query packing, the split-KV
+    stream of every request's context, and the combine that attends the verify tokens
+    and merges."""
+    import ctypes
+
+    from flashmap_amd import _native, ops
+
+    batch, hq, hkv, d, length, lo, hi, mask = VERIFY_WORKLOADS[args.workload]
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(lo, hi + 1, (batch,), generator=g)
+    ctx = int(lens.sum())
+    slots = torch.randperm(ctx, generator=g).to(torch.int32)
+    q = torch.randn(batch * length, hq, d, generator=g).bfloat16().to(dev)
+    k_ext = torch.randn(batch * length, hkv, d, generator=g).bfloat16().to(dev)
+    v_ext = torch.randn(batch * length, hkv, d, generator=g).bfloat16().to(dev)
+    kb = torch.empty(ctx, hkv, d, dtype=torch.bfloat16, device=dev)
+    vb = torch.empty_like(kb)
+    chunk = 1 << 15
+    for s in range(0, ctx, chunk):  # bounded fp32 temporaries
+        e = min(ctx, s + chunk)
+        kb[slots[s:e].long().to(dev)] = torch.randn(e - s, hkv, d, generator=g).bfloat16().to(dev)
+        vb[slots[s:e].long().to(dev)] = torch.randn(e - s, hkv, d, generator=g).bfloat16().to(dev)
+    indptr = torch.zeros(batch + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    indptr, indices = indptr.to(dev), slots.to(dev)
+    cmask = None
+    if mask == "qlen":
+        tril = torch.ones(length, length, dtype=torch.bool).tril()
+        cmask = tril.reshape(-1).repeat(batch).to(dev)
+    out = torch.empty_like(q)
+
+    def call():
+        ops.verify_attention(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, None, mask == "qlen", out=out,
+                             max_context=hi)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    lib = _native.lib()
+    lib.fm_profile_enable(1)
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    tot, cnt = ctypes.c_double(), ctypes.c_int64()
+    _native.call("fm_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
+    lib.fm_profile_enable(0)
+    kernel_ms = tot.value / max(cnt.value, 1)
+    kv = ctx * hkv * d * 2 * 2
+    total = kv + 4 * ctx + 4 * (batch + 1) + 2 * batch * length * hq * d * 2 + batch * length * hkv * d * 2 * 2
+    achieved = total / (kernel_ms * 1e-3) / 1e9
+    result = {
+        "metric": "target verify attn µs/call + achieved HBM TB/s, 17 verify tokens, batch 64, ctx 256–8k, 1 GPU",
+        "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: seeded CPU draw (lengths, pool slots, q, K/V)",
+        "config": {"workload": args.workload, "batch": batch, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+                   "verify_tokens": length, "ctx_lo": lo, "ctx_hi": hi, "ctx_sum": ctx, "mask": mask,
+                   "layout": "sglang token pool (pool, kv_heads, head_dim), kv_indptr/kv_indices"},
+        "hbm_tbs": round(total / (ms * 1e-3) / 1e12, 3),
+        "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": total, "kernel_us": round(kernel_ms * 1e3, 2)},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = verify_cpu_baseline(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, mask, lens,
+                                                     length, args.cpu_budget)
+    return result
+
+
+def verify_cpu_baseline(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, mask, lens, length, budget_s) -> dict:
+    """The verify oracle on the host cores, request by request until the budget is
+    spent, scaled to the whole call by context positions."""
+    from oracle import attention as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    ip, idx = indptr.cpu(), indices.cpu()
+    done_l = done = 0
+    t0 = time.perf_counter()
+    for b in range(len(lens)):
+        lo_, hi_ = int(ip[b]), int(ip[b + 1])
+        rows = idx[lo_:hi_].long()
+        sub_ip = torch.tensor([0, hi_ - lo_], dtype=torch.int32)
+        tok = slice(b * length, (b + 1) * length)
+        sub_mask = None if cmask is None else cmask.cpu()[b * length * length:(b + 1) * length * length]
+        ref.verify_attention(q[tok].cpu(), k_ext[tok].cpu(), v_ext[tok].cpu(), kb[rows.to(kb.device)].cpu(),
+                             vb[rows.to(vb.device)].cpu(), sub_ip, torch.arange(hi_ - lo_), sub_mask, None,
+                             mask == "qlen")
+        done_l += hi_ - lo_
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    return {"value": round(elapsed * int(lens.sum()) / done_l * 1e6, 1), "unit": "us/call", "cores": cores,
+            "kind": "port", "sample": f"first {done} of {len(lens)} requests ({done_l} context positions): "
+                                      "fp32 oracle verify attention, scaled by positions"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64", choices=sorted(WORKLOADS) + sorted(VERIFY_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", type=int, default=0,
@@ -175,6 +290,10 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": src.numel(), "copies": args.calibrate_copy}))
+        return 0
+
+    if args.workload in VERIFY_WORKLOADS:
+        print(json.dumps(run_verify(args, dev)))
         return 0
 
     from flashmap_amd import _native, ops

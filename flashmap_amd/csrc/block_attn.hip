@@ -97,6 +97,8 @@ struct AttnArgs {
   int32_t nrb;                       // 16-row blocks (wavefronts) per unit
   int32_t num_shares;  // workgroups x replicas
   float scale_log2;
+  float v_scale;  // combine: scale of the context partials' values (1 but for verify calls)
+  int32_t tail;   // verify calls: unit u's verify-token partial is slot units + num_shares + u
   const uint16_t *qp;  // packed queries: (units, 16 nrb rows, D) bf16, invalid rows 0
   uint16_t *part_o;    // partials: (units + num_shares, 16 nrb, D) fp16, rows / their scale
   float *part_lse;     // (units + num_shares, 16 nrb, 2): log2-domain LSE, row scale
@@ -503,6 +505,10 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
   }
 }
 
+template <int D>
+__device__ __forceinline__ void pv_accumulate(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
+                                              int lane);
+
 // One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T.
 template <int D>
 __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stage,
@@ -554,6 +560,16 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
   l += ps;
   const u32x4_t pk = {pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
                       pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+  pv_accumulate<D>(stage + G::KBYTES, pk, acc, lane);
+}
+
+// O^T += V^T P^T for one tile: pk holds this lane's bf16 P^T values (row n, positions
+// 16 pb + 4 g + i), vbase the tile's V blocks in the stage layout.
+template <int D>
+__device__ __forceinline__ void pv_accumulate(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
+                                              int lane) {
+  using G = Geo<D>;
+  const int n = lane & 15, g = lane >> 4;
   // V^T operand: row d = 16 db + n, reduction positions pos(g, j) = 4g + j (j < 4) and
   // 16 + 4g + j - 4 (j >= 4), the positions of this lane's S^T values. Two
   // ds_read_b64_tr_b16 per operand: within each 16-lane group, lane l receives slot j
@@ -565,14 +581,14 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
   for (int hh = 0; hh < 2; ++hh) {
     const int r = 16 * hh + 4 * g + s4;
     const int blk = (r & 3) + 4 * (r / (4 * G::RPB)), slot = (r % (4 * G::RPB)) >> 2;
-    vb[hh] = G::KBYTES + blk * G::VPITCH + slot * (2 * D) + 8 * c4;
+    vb[hh] = blk * G::VPITCH + slot * (2 * D) + 8 * c4;
   }
   // The reads are issued as inline asm with their own lgkmcnt wait: through the
   // builtin, the compiler cannot tell them apart from the LDS-DMA writes still in
   // flight for later tiles and drains those (vmcnt(0)) before every tile's P.V.
   typedef __attribute__((address_space(3))) const char lds_char_t;
-  const uint32_t a0 = (uint32_t)(uintptr_t)(lds_char_t *)(stage + vb[0]);
-  const uint32_t a1 = (uint32_t)(uintptr_t)(lds_char_t *)(stage + vb[1]);
+  const uint32_t a0 = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + vb[0]);
+  const uint32_t a1 = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + vb[1]);
   u32x2_t w[2][G::DB];
 #pragma unroll
   for (int db = 0; db < G::DB; ++db) {
@@ -598,13 +614,30 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
   }
 }
 
+// The verify tokens' own keys and values and the mask among them (target verification:
+// every request has q_len tokens that see its whole context and, among themselves,
+// what the mask allows).
+struct VerifyArgs {
+  const uint16_t *k, *v;  // (batch * q_len, kv heads, D): token b * q_len + j
+  int64_t k_st, k_sh, v_st, v_sh;
+  const uint8_t *mask;         // mode 1 / 2; nonzero = visible
+  const int64_t *mask_indptr;  // mode 1: start of request b's mask rows
+  int32_t mode;                // 0 causal, 1 rows of context + q_len entries, 2 q_len x q_len blocks
+  float scale_log2;            // softmax_scale * log2(e) of the tokens' scores
+};
+
+template <int D>
+__device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArgs &v, const u32x4_t (&qf)[D / 32], char *vs,
+                              int64_t unit, int b, int h, int rg, int rb, int lane);
+
 // The query rows of every unit in MFMA-block order: row r of unit (b, h, rg) is query
 // head h*G + R / q_len at draft token R % q_len, R = rg * 16 nrb + r, rows beyond the
 // group or the sequence's draft rows are zero. With the prologue requested, each row
 // is QK-RMSNormed and rotated at its position (the code the standalone prologue runs,
-// so the values are bit-identical to it). One wavefront per 16-row block.
-template <int D>
-__global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a) {
+// so the values are bit-identical to it). One wavefront per 16-row block. VERIFY: the
+// wavefront then attends its rows to their request's verify tokens (verify_tokens).
+template <int D, bool VERIFY>
+__global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, const VerifyArgs v) {
   constexpr int KT = D / 32;
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();  // (unit, row block)
@@ -633,6 +666,14 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a) {
   uint16_t *dst = const_cast<uint16_t *>(a.qp) + (unit * 16 * a.nrb + r) * D + 8 * g;
 #pragma unroll
   for (int t = 0; t < KT; ++t) store16(dst + 32 * t, valid ? qf[t] : u32x4_t{0, 0, 0, 0});
+  if constexpr (VERIFY) {
+    using G = Geo<D>;
+    __shared__ __attribute__((aligned(1024))) char vstage[4][G::VBLKS * G::VPITCH];
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+      if (!valid) qf[t] = u32x4_t{0, 0, 0, 0};
+    verify_tokens<D>(a, v, qf, vstage[wave_id()], unit, b, h, rg, rb, lane);
+  }
 }
 
 // A segment's partial for this wavefront's 16 rows: O = acc * inv as fp16 of O / scale,
@@ -668,6 +709,95 @@ __device__ __forceinline__ void store_partial_rows(const AttnArgs &a, const u32x
     *reinterpret_cast<__attribute__((address_space(1))) u32x2_t *>(dst + 16 * db) = h[db];
   if (g == 0)
     *reinterpret_cast<__attribute__((address_space(1))) f32x2_t *>((gfloat *)a.part_lse + 2 * row) = f32x2_t{lse, sc};
+}
+
+// The verify tokens' part of a verify call for one wavefront's 16 rows (lane (n, g):
+// row n, query fragments qf in the streaming kernel's layout): the rows attend to their
+// request's q_len tokens under the mask, TILE tokens at a time -- keys loaded straight
+// into registers in the K-operand layout, values staged in this wavefront's LDS slice
+// vs in the stage's V layout -- and the result is stored as the unit's tail partial
+// (O / scale in fp16, log2-domain LSE; -inf for a row that sees no token). Tokens past
+// q_len read the last token (finite) and get P = 0. No branch surrounds the MFMA or the
+// transposing LDS reads, which need every lane.
+template <int D>
+__device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArgs &v, const u32x4_t (&qf)[D / 32], char *vs,
+                              int64_t unit, int b, int h, int rg, int rb, int lane) {
+  using G = Geo<D>;
+  constexpr int KT = D / 32;
+  const int n = lane & 15, g = lane >> 4;
+  const int L = a.q_len;
+  const int rows = a.nrb * 16;
+  const int64_t tok0 = (int64_t)b * L;
+  const int R = rg * rows + rb * 16 + n;
+  const int tq = R - (R / L) * L;  // row n's verify token
+  int64_t mrow = 0;                // mask entry of (token tq, token 0)
+  if (v.mode == 1) {
+    const int ctx = a.seqlens[b + 1] - a.seqlens[b];  // CSR: indptr
+    mrow = v.mask_indptr[b] + (int64_t)tq * (ctx + L) + ctx;
+  } else if (v.mode == 2) {
+    mrow = (tok0 + tq) * L;
+  }
+  const uint16_t *kb = v.k + (int64_t)h * v.k_sh;
+  const uint16_t *vb = v.v + (int64_t)h * v.v_sh;
+  f32x4_t acc[G::DB];
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  for (int j0 = 0; j0 < L; j0 += TILE) {
+    const int last = L - 1 - j0;  // last token of the chunk
+#pragma unroll
+    for (int i = G::KFRAGS; i < G::NI; ++i) {  // values, as the stage's V blocks
+      int row, coff, dst;
+      bool isk;
+      load_slot<D>(i, lane, row, coff, isk, dst);
+      const int j = j0 + (row < last ? row : last);
+      *reinterpret_cast<u32x4_t *>(vs + (dst - G::KBYTES) + lane * 16) = load16(vb + (tok0 + j) * v.v_st + coff);
+    }
+    f32x4_t s[2];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {  // S^T[token 16 pb + 4 g + i][row n]
+      const int jr = 16 * pb + n;
+      const uint16_t *kr = kb + (tok0 + j0 + (jr < last ? jr : last)) * v.k_st + 8 * g;
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) c = mfma_16x16x32(load16(kr + 32 * t), qf[t], c);
+      s[pb] = c;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = j0 + 16 * pb + 4 * g + i;
+        const bool seen = j < L && (v.mode == 0 ? j <= tq : v.mask[mrow + j] != 0);
+        s[pb][i] = seen ? s[pb][i] * v.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, s[pb][i]);
+      }
+    const float mn = fmaxf(m, max_over_groups(mx));
+    const float alpha = mn > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 1.f;  // 0 at the first seen token
+    l *= alpha;
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db) acc[db] *= alpha;
+    float p[2][4];
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[pb][i] = s[pb][i] > -INFINITY ? __builtin_amdgcn_exp2f(s[pb][i] - mn) : 0.f;
+        l += p[pb][i];
+      }
+    m = mn;
+    const u32x4_t pk = {pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
+                        pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
+    asm volatile("" ::: "memory");  // the value stores above precede the transposing reads
+    pv_accumulate<D>(vs, pk, acc, lane);
+  }
+  const float lt = sum_over_groups(l);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  const float lse = lt > 0.f ? m + log2f(lt) : -INFINITY;
+  u32x2_t hp[G::DB];
+  const float sc = make_partial<D>(acc, inv, hp);
+  store_partial_rows<D>(a, hp, lse, sc, ((int64_t)a.batch * a.ups + a.num_shares + unit) * rows + rb * 16 + n, g);
 }
 
 // The hand-off of partials from the consumers to the producer: an LDS slot of the
@@ -1063,101 +1193,25 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
   const int gq = R / a.q_len, tq = R - gq * a.q_len;
   if (gq >= a.group || tq >= qlen_b) return;
   RowMerge mg;
-  merge_partials<D>(a, unit, b, ul, r, c, 1.f, mg);
+  merge_partials<D>(a, unit, b, ul, r, c, a.v_scale, mg);
+  if (a.tail) {  // the verify tokens' partial
+    typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+    const int64_t row = ((int64_t)a.batch * a.ups + a.num_shares + unit) * rows + r;
+    const f32x2_t ls = *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row);
+    const u32x4_t ow = load16(a.part_o + row * D + 8 * c);
+    if (ls[0] != -INFINITY) {
+      f32x4_t x[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        x[j] = f32x4_t{f16_lo(ow[2 * j]), f16_hi(ow[2 * j]), f16_lo(ow[2 * j + 1]), f16_hi(ow[2 * j + 1])};
+      mg.add(ls[0], ls[1], 1.f, x);
+    }
+  }
   mg.finish();
   const int64_t head = (int64_t)h * a.group + gq;
   store_row8(a.o + (a.cu_q ? (first_tok + tq) * a.o_st : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
                  head * a.o_sh + 8 * c,
              mg.acc);
-}
-
-// The verify tokens' own keys and values and the mask among them (target verification:
-// every request has q_len tokens that see its whole context and, among themselves,
-// what the mask allows).
-struct VerifyArgs {
-  const uint16_t *k, *v;  // (batch * q_len, kv heads, D): token b * q_len + j
-  int64_t k_st, k_sh, v_st, v_sh;
-  const uint8_t *mask;         // mode 1 / 2; nonzero = visible
-  const int64_t *mask_indptr;  // mode 1: start of request b's mask rows
-  int32_t mode;                // 0 causal, 1 rows of context + q_len entries, 2 q_len x q_len blocks
-  float scale_log2;            // softmax_scale * log2(e) of the tokens' scores
-  float v_scale;               // scale of the context's values
-};
-
-// Sum over the C lanes that hold one row (consecutive lanes, C a power of two <= 16).
-template <int C>
-__device__ __forceinline__ float row_sum(float x) {
-#pragma unroll
-  for (int o = C / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
-// The combine of a verify call: each row's attention to its request's verify tokens
-// (at most q_len keys, masked), merged with the context partials of the streaming
-// kernel. Same thread layout as attn_combine_kernel; every lane stays active to the
-// end (the row sums cross lanes), rows past the group store nothing.
-template <int D>
-__global__ __launch_bounds__(2 * D) void verify_combine_kernel(const AttnArgs a, const VerifyArgs v) {
-  constexpr int C = D / 8;
-  const int rows = a.nrb * 16;
-  const int64_t unit = blockIdx.x / a.nrb;
-  const int r = (int)(blockIdx.x - unit * a.nrb) * 16 + (int)threadIdx.x / C;
-  const int c = (int)threadIdx.x % C;
-  const int b = (int)(unit / a.ups);
-  const int ul = (int)(unit - (int64_t)b * a.ups);
-  const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
-  const int L = a.q_len;
-  const int R = rg * rows + r;
-  const int gq = R / L, tq = R - gq * L;
-  const bool valid = gq < a.group;
-  RowMerge mg;
-  merge_partials<D>(a, unit, b, ul, r, c, v.v_scale, mg);
-  // The row's query (packed rows: zero past the group).
-  const u32x4_t qw = load16(a.qp + (unit * rows + r) * D + 8 * c);
-  float q[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) q[2 * j] = bf16_lo(qw[j]), q[2 * j + 1] = bf16_hi(qw[j]);
-  const int64_t tok0 = (int64_t)b * L;
-  const uint16_t *kb = v.k + h * v.k_sh + 8 * c;
-  const uint16_t *vb = v.v + h * v.v_sh + 8 * c;
-  int64_t mrow = 0;  // mask entry of (row tq, token 0)
-  if (v.mode == 1) {
-    const int ctx = a.seqlens[b + 1] - a.seqlens[b];  // CSR: indptr
-    mrow = v.mask_indptr[b] + (int64_t)tq * (ctx + L) + ctx;
-  } else if (v.mode == 2) {
-    mrow = (tok0 + tq) * L;
-  }
-  auto score = [&](int j) {
-    const u32x4_t kw = load16(kb + (tok0 + j) * v.k_st);
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s += q[2 * i] * bf16_lo(kw[i]) + q[2 * i + 1] * bf16_hi(kw[i]);
-    return row_sum<C>(s) * v.scale_log2;
-  };
-  auto visible = [&](int j) { return v.mode == 0 ? j <= tq : v.mask[mrow + j] != 0; };
-  float mt = -INFINITY;
-  for (int j = 0; j < L; ++j) {
-    const float s = score(j);
-    if (visible(j)) mt = fmaxf(mt, s);
-  }
-  // (A row with no visible token has mt = -inf and p = 0 throughout; no branch, so the
-  // row sums never run under divergence.)
-  f32x4_t at[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  float lt = 0.f;
-  for (int j = 0; j < L; ++j) {
-    const float s = score(j);
-    const float p = visible(j) ? __builtin_amdgcn_exp2f(s - mt) : 0.f;
-    lt += p;
-    const float pb = round_bf16(p);  // P . V in bf16 operands
-    const u32x4_t vw = load16(vb + (tok0 + j) * v.v_st);
-    at[0] += f32x4_t{bf16_lo(vw[0]), bf16_hi(vw[0]), bf16_lo(vw[1]), bf16_hi(vw[1])} * pb;
-    at[1] += f32x4_t{bf16_lo(vw[2]), bf16_hi(vw[2]), bf16_lo(vw[3]), bf16_hi(vw[3])} * pb;
-  }
-  if (lt > 0.f) mg.add(mt, 1.f, lt, at);
-  mg.finish();
-  if (!valid) return;
-  const int64_t head = (int64_t)h * a.group + gq;
-  store_row8(a.o + (int64_t)b * a.o_sb + (int64_t)tq * a.o_st + head * a.o_sh + 8 * c, mg.acc);
 }
 
 // plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(L_b, 0) / TILE), L_b = seqlens[b], or
@@ -1261,8 +1315,9 @@ struct Sizing {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// tail: a verify call (one more partial slot per unit, for its verify tokens).
 static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int max_k,
-                  bool need_plan, Sizing *sz) {
+                  bool need_plan, Sizing *sz, bool tail = false) {
   DeviceInfo info;
   int rc = device_info(&info);
   if (rc != FM_OK) return rc;
@@ -1282,7 +1337,7 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->num_shares = (int)nw * r;
   const size_t rows = (size_t)sz->rp.nrb * 16;
   const size_t units = (size_t)batch * ups;
-  const size_t slots = units + (size_t)sz->num_shares;  // partial slot unit + share
+  const size_t slots = units + (size_t)sz->num_shares + (tail ? units : 0);  // unit + share; tails
   size_t off = 0;
   sz->plan_off = off;
   if (need_plan) off = align256(off + sizeof(int32_t) * ((size_t)batch + 1));
@@ -1348,7 +1403,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   const bool need_plan = a.seqlens != nullptr && c.plan == nullptr;
   Sizing sz;
-  int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz);
+  int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr);
   if (rc != FM_OK) return rc;
   if (c.ws == nullptr || c.ws_bytes < sz.bytes)
     return fail(FM_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", c.ws_bytes, sz.bytes);
@@ -1374,6 +1429,8 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   a.q_pos = c.q_pos;
   a.eps = c.eps;
   a.num_shares = sz.num_shares;
+  a.tail = vf != nullptr;
+  if (!a.tail) a.v_scale = 1.f;
   char *ws = (char *)c.ws;
   a.qp = (const uint16_t *)(ws + sz.q_off);
   a.part_lse = (float *)(ws + sz.lse_off);
@@ -1392,10 +1449,15 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     a.uniform_tiles = (a.uniform_len + TILE - 1) / TILE;
   }
   const int64_t qblocks = (units * sz.rp.nrb + 3) / 4;
-  if (c.d == 128)
-    pack_queries_kernel<128><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
+  const VerifyArgs nov{};
+  if (vf != nullptr && c.d == 128)
+    pack_queries_kernel<128, true><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, *vf);
+  else if (vf != nullptr)
+    pack_queries_kernel<64, true><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, *vf);
+  else if (c.d == 128)
+    pack_queries_kernel<128, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
   else
-    pack_queries_kernel<64><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
+    pack_queries_kernel<64, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
   FM_CHECK_HIP(hipGetLastError());
   AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb);
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
@@ -1408,16 +1470,10 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // One workgroup of 2 D threads per 16-row block.
   const int64_t cblocks = units * sz.rp.nrb;
   FM_REQUIRE(cblocks < (1ll << 31), "too many units");
-  if (vf != nullptr) {
-    if (c.d == 128)
-      verify_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a, *vf);
-    else
-      verify_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(128), 0, c.stream>>>(a, *vf);
-  } else if (c.d == 128) {
+  if (c.d == 128)
     attn_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
-  } else {
+  else
     attn_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(128), 0, c.stream>>>(a);
-  }
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
@@ -1580,7 +1636,7 @@ extern "C" size_t fm_verify_workspace_bytes(int32_t batch, int32_t verify_len, i
   if (device != prev && hipSetDevice(device) != hipSuccess) return 0;
   Sizing sz;
   const int rc = sizing(PAGED, batch, verify_len, num_q_heads, num_kv_heads, head_dim,
-                        verify_max_context(max_context, pool_size), true, &sz);
+                        verify_max_context(max_context, pool_size), true, &sz, true);
   if (device != prev) hipSetDevice(prev);
   return rc == FM_OK ? sz.bytes : 0;
 }
@@ -1628,8 +1684,9 @@ extern "C" int fm_verify_attention(
   a.csr = 1;
   a.id_shift = kv_index_bytes == 8 ? 1 : 0;
   a.seqlens = kv_indptr;
+  a.v_scale = v_scale;
   VerifyArgs vf{(const uint16_t *)k_ext, (const uint16_t *)v_ext, k_ext_stride_token, k_ext_stride_head,
                 v_ext_stride_token, v_ext_stride_head, custom_mask, mask_indptr, mask_mode,
-                sm_scale * 1.4426950408889634f, v_scale};
+                sm_scale * 1.4426950408889634f};
   return run_attention(c, PAGED, a, &vf);
 }
