@@ -219,6 +219,12 @@ def run_verify(args, dev) -> dict:
     kv = ctx * hkv * d * 2 * 2
     total = kv + 4 * ctx + 4 * (batch + 1) + 2 * batch * length * hq * d * 2 + batch * length * hkv * d * 2 * 2
     achieved = total / (kernel_ms * 1e-3) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / f"attn_fwd_{args.workload.replace('-qwen3-8b-', '_').replace('-', '_')}.traffic.json"
+    if tfile.exists():
+        rec = json.loads(tfile.read_text())
+        if rec.get("workload") == args.workload:
+            traffic = rec["traffic_bytes"]
     result = {
         "metric": "target verify attn µs/call + achieved HBM TB/s, 17 verify tokens, batch 64, ctx 256–8k, 1 GPU",
         "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -230,7 +236,7 @@ def run_verify(args, dev) -> dict:
         "hbm_tbs": round(total / (ms * 1e-3) / 1e12, 3),
         "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": total, "kernel_us": round(kernel_ms * 1e3, 2)},
+                     "traffic": traffic, "bytes_per_launch": total, "kernel_us": round(kernel_ms * 1e3, 2)},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = verify_cpu_baseline(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, mask, lens,
