@@ -53,6 +53,16 @@ SIGNATURES: dict[str, tuple] = {
         [*_Q, P, P, I64, I64, I64, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,
          *_PROLOGUE, *_SPLIT],
     ),
+    "fm_block_attn_paged_fp8": (
+        c_int,
+        [P, I32, I64, I64, I64, P, I64, I64, I64, P, P, I64, I64, I64, I64, I64, I32, P, I64, I64, P,
+         I32, I32, I32, I32, I32, I32, F32, P, I64, I64, I64, *_PROLOGUE, *_SPLIT],
+    ),
+    "fm_block_attn_token_paged_fp8": (
+        c_int,
+        [P, I32, I64, I64, I64, P, I64, I64, I64, P, P, P, I64, I64, I64, I64, I64, P, I64, I64, P,
+         I32, I32, I32, I32, I32, I32, F32, P, I64, I64, I64, *_PROLOGUE, *_SPLIT],
+    ),
     "fm_verify_workspace_bytes": (c_size_t, [I32, I32, I32, I32, I32, I32, I64, c_int]),
     "fm_verify_attention": (
         c_int,
@@ -68,6 +78,13 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "fm_write_context_kv_pool": (
         c_int, [P, I64, I32, I32, I32, P, P, *_ROPE, P, P, P, I64, F32, P]
+    ),
+    "fm_write_context_kv_fp8": (
+        c_int,
+        [P, I64, I32, I32, I32, P, P, P, *_ROPE, P, I32, I32, I64, I64, I64, I64, I32, P, F32, P],
+    ),
+    "fm_write_context_kv_pool_fp8": (
+        c_int, [P, I64, I32, I32, I32, P, P, *_ROPE, P, P, P, I64, F32, F32, F32, P]
     ),
     "fm_profile_enable": (c_int, [c_int]),
     "fm_profile_read": (c_int, [ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]),

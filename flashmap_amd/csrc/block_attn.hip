@@ -66,8 +66,8 @@ enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 
 // K/V geometry of the units.
 struct UnitArgs {
-  const uint16_t *k;
-  const uint16_t *v;
+  const char *k;  // bytes (the element size is the kernel's)
+  const char *v;
   int64_t k_s0, k_s1;  // CONTIG: batch, head; paged: page (slot), head (elements)
   int64_t v_s0, v_s1;
   int64_t table_stride;
@@ -99,6 +99,14 @@ struct AttnArgs {
   float scale_log2;
   float v_scale;  // combine: scale of the context partials' values (1 but for verify calls)
   int32_t tail;   // verify calls: unit u's verify-token partial is slot units + num_shares + u
+  // FP8 K/V: the packed queries are e4m3 with a score scale per row (q_rs: (units, 16 nrb)
+  // floats); descales (q, k, v) per (sequence, KV head) at [b * sb + h * sh] (NULL: 1);
+  // q_fp8: the caller's queries are e4m3 already (else bf16, quantized per (sequence,
+  // query head) with scale amax / 448).
+  int32_t f8, q_fp8;
+  float *q_rs;
+  const float *qd, *kd, *vd;
+  int64_t d_sb, d_sh;
   const uint16_t *qp;  // packed queries: (units, 16 nrb rows, D) bf16, invalid rows 0
   uint16_t *part_o;    // partials: (units + num_shares, 16 nrb, D) fp16, rows / their scale
   float *part_lse;     // (units + num_shares, 16 nrb, 2): log2-domain LSE, row scale
@@ -123,15 +131,25 @@ struct AttnArgs {
 // of block v holds row 4*RPB*(v/4) + 4k + v%4), blocks padded by 32 bytes: the four
 // consecutive rows one ds_read_b64_tr_b16 of the P.V operand touches then sit in four
 // blocks on disjoint banks. The stage ends with the tile's 32 page ids (paged layouts).
-template <int D>
+//
+// FP8 (e4m3 K/V, one byte per element): K block (pb, c) holds bytes 64 c .. 64 c + 63 of
+// rows 16 pb + n at lane*16 (16 channels: the fp8 MFMA operands of two 32-channel
+// k-steps); V block v holds rows RPB v .. RPB v + RPB - 1 by rows, the 16-byte chunk c of
+// row r at chunk c ^ swz(r) (swz(r) = (r / rows per 256 bytes) mod LPR), so that the
+// transposing ds_read_b64_tr_b8 of one 16-channel block spreads over the banks.
+template <int D, bool F8 = false>
 struct Geo {
-  static constexpr int KT = D / 32;            // k-steps over head_dim
+  static constexpr int ES = F8 ? 1 : 2;        // bytes per element
+  static constexpr int RB = D * ES;            // bytes per row
+  static constexpr int KT = D / 32;            // bf16 k-steps over head_dim
+  static constexpr int KC = RB / 64;           // 64-byte slices of a row (K blocks per 16 rows)
   static constexpr int DB = D / 16;            // 16-channel blocks of O^T
-  static constexpr int KFRAGS = 2 * KT;        // 1 KB K blocks per tile
-  static constexpr int LPR = D / 8;            // 16-byte chunks per row
+  static constexpr int KFRAGS = 2 * KC;        // 1 KB K blocks per tile
+  static constexpr int LPR = RB / 16;          // 16-byte chunks per row
   static constexpr int RPB = 64 / LPR;         // V rows per 1 KB block
   static constexpr int VBLKS = TILE / RPB;     // V blocks per tile
-  static constexpr int VPITCH = 1024 + 32;     // bytes per V block (with pad)
+  static constexpr int VPITCH = F8 ? 1024 : 1024 + 32;  // bytes per V block (bf16: with pad)
+  static constexpr int R256 = 256 / RB;        // FP8: rows per 256 bytes (the swizzle period)
   static constexpr int NI = KFRAGS + VBLKS;    // 16-byte LDS-DMA loads per lane per tile
   static constexpr int KBYTES = KFRAGS * 1024;
   static constexpr int VBYTES = VBLKS * VPITCH;
@@ -363,10 +381,10 @@ __device__ __forceinline__ void block_sync() {
 // positions or a multiple: the pages of the two 16-position halves; otherwise (e.g.
 // SGLang's token pool): the page of each of the 32 positions. Positions are clamped
 // to the sequence, columns to the table.
-template <int LAYOUT, int D>
+template <int LAYOUT, int D, bool F8 = false>
 __device__ __forceinline__ void issue_ids(const AttnArgs &a, const int32_t *__restrict__ table,
                                           const Cursor &c, char *stage, int lane) {
-  using G = Geo<D>;
+  using G = Geo<D, F8>;
   const int32_t *row = table + (c.row << a.id_shift);
   const int last = c.L - 1 > 0 ? c.L - 1 : 0;
   if (LAYOUT == PAGED16) {
@@ -395,52 +413,58 @@ struct Loader {
   const char *kb, *vb;
 };
 
-template <int LAYOUT>
+template <int LAYOUT, int ES = 2>
 __device__ __forceinline__ void loader_unit(const AttnArgs &a, Loader &ld) {
   const UnitArgs &ua = a.u;
   const int64_t h = ld.c.h;
   if (LAYOUT == CONTIG) {
     ld.cap = ua.pos_cap;
     ld.lim = ld.c.L < ua.pos_cap ? ld.c.L : ua.pos_cap;
-    ld.kb = reinterpret_cast<const char *>(ua.k + (int64_t)ld.c.b * ua.k_s0 + h * ua.k_s1);
-    ld.vb = reinterpret_cast<const char *>(ua.v + (int64_t)ld.c.b * ua.v_s0 + h * ua.v_s1);
+    ld.kb = ua.k + ((int64_t)ld.c.b * ua.k_s0 + h * ua.k_s1) * ES;
+    ld.vb = ua.v + ((int64_t)ld.c.b * ua.v_s0 + h * ua.v_s1) * ES;
   } else {
     ld.lim = ld.c.L;
-    ld.kb = reinterpret_cast<const char *>(ua.k + h * ua.k_s1);
-    ld.vb = reinterpret_cast<const char *>(ua.v + h * ua.v_s1);
+    ld.kb = ua.k + h * ua.k_s1 * ES;
+    ld.vb = ua.v + h * ua.v_s1 * ES;
   }
 }
 
-template <int LAYOUT>
+template <int LAYOUT, int ES = 2>
 __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<LAYOUT != CONTIG> &sm,
                                                Loader &ld) {
-  if (cursor_next(a, sm, ld.c)) loader_unit<LAYOUT>(a, ld);
+  if (cursor_next(a, sm, ld.c)) loader_unit<LAYOUT, ES>(a, ld);
 }
 
-// Row (within the tile) and channel offset of this lane's k-th load of a tile, and
-// whether it is a K load. Load i = wave + k*W of the NI loads (K blocks, then V blocks).
-template <int D>
+// Row (within the tile) and byte offset within the row of this lane's k-th load of a
+// tile, and whether it is a K load. Load i = wave + k*W of the NI loads (K blocks, then
+// V blocks).
+template <int D, bool F8 = false>
 __device__ __forceinline__ void load_slot(int i, int lane, int &row, int &coff, bool &isk, int &dst) {
-  using G = Geo<D>;
+  using G = Geo<D, F8>;
   const int n = lane & 15, g = lane >> 4;
   isk = i < G::KFRAGS;
   if (isk) {
-    const int pb = i / G::KT, t = i - (i / G::KT) * G::KT;
+    const int pb = i / G::KC, c = i - (i / G::KC) * G::KC;
     row = 16 * pb + n;
-    coff = 32 * t + 8 * g;
+    coff = 64 * c + 16 * g;
     dst = i * 1024;
   } else {
     const int vb = i - G::KFRAGS;
-    row = 4 * G::RPB * (vb / 4) + 4 * (lane / G::LPR) + (vb % 4);
-    coff = 8 * (lane % G::LPR);
+    if constexpr (F8) {
+      row = vb * G::RPB + lane / G::LPR;
+      coff = 16 * ((lane % G::LPR) ^ ((row / G::R256) % G::LPR));
+    } else {
+      row = 4 * G::RPB * (vb / 4) + 4 * (lane / G::LPR) + (vb % 4);
+      coff = 16 * (lane % G::LPR);
+    }
     dst = G::KBYTES + vb * G::VPITCH;
   }
 }
 
-template <int LAYOUT, int D, int W>
+template <int LAYOUT, int D, int W, bool F8 = false>
 __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, char *stage, int wave,
-                                         int lane, const uint32_t (&loff)[(Geo<D>::NI + W - 1) / W]) {
-  using G = Geo<D>;
+                                         int lane, const uint32_t (&loff)[(Geo<D, F8>::NI + W - 1) / W]) {
+  using G = Geo<D, F8>;
   constexpr int KPW = (G::NI + W - 1) / W;
   const int pos0 = ld.c.lt * TILE;
   const int32_t *ids = reinterpret_cast<const int32_t *>(stage + G::KBYTES + G::VBYTES);
@@ -469,7 +493,7 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
       if (i >= G::NI) break;
       int row, coff, dst;
       bool isk;
-      load_slot<D>(i, lane, row, coff, isk, dst);
+      load_slot<D, F8>(i, lane, row, coff, isk, dst);
       const int hp = row >> 4;  // uniform except for head_dim 64's V blocks
       const char *base = isk ? (hp ? kh[1] : kh[0]) : (hp ? vh[1] : vh[0]);
       dma16(base + loff[k], stage + dst);
@@ -484,7 +508,7 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
     if (i >= G::NI) break;
     int row, coff, dst;
     bool isk;
-    load_slot<D>(i, lane, row, coff, isk, dst);
+    load_slot<D, F8>(i, lane, row, coff, isk, dst);
     row = row < last ? row : last;
     const char *base = isk ? ld.kb : ld.vb;
     const uint32_t tok_b = isk ? a.k_tok_b : a.v_tok_b;
@@ -501,29 +525,41 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
       const uint32_t in_page = a.page_size == 1 ? 0u : (uint32_t)(p - (p / a.page_size) * a.page_size);
       off = (uint64_t)page * (isk ? a.k_page_b : a.v_page_b) + in_page * tok_b;
     }
-    dma16(base + off + 2 * coff, stage + dst);
+    dma16(base + off + coff, stage + dst);
   }
 }
 
 template <int D>
 __device__ __forceinline__ void pv_accumulate(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
                                               int lane);
-
-// One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T.
 template <int D>
+__device__ __forceinline__ void pv_accumulate_f8(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
+                                                 int lane);
+
+// One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T. sl:
+// this lane's row's score scale in log2 units (softmax_scale log2(e), times the row's
+// query and key descales with fp8 K/V). F8: K and Q are e4m3 (the fp8 MFMA, each 16-byte
+// fragment the operands of two k-steps), V e4m3 widened to bf16 after the transposing
+// read; P is bf16 either way.
+template <int D, bool F8 = false>
 __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stage,
-                                             const u32x4_t (&qf)[D / 32], f32x4_t (&acc)[D / 16],
+                                             const u32x4_t (&qf)[Geo<D, F8>::KC], float sl, f32x4_t (&acc)[D / 16],
                                              float &m, float &l, int pos0, int L, int lane) {
-  using G = Geo<D>;
-  const int n = lane & 15, g = lane >> 4;
+  using G = Geo<D, F8>;
+  const int g = lane >> 4;
   f32x4_t s[2];
 #pragma unroll
   for (int pb = 0; pb < 2; ++pb) {
     f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < G::KT; ++t) {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(stage + (pb * G::KT + t) * 1024 + lane * 16);
-      c = mfma_16x16x32(kf, qf[t], c);
+    for (int t = 0; t < G::KC; ++t) {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(stage + (pb * G::KC + t) * 1024 + lane * 16);
+      if constexpr (F8) {
+        c = mfma_16x16x32_f8(u32x2_t{kf[0], kf[1]}, u32x2_t{qf[t][0], qf[t][1]}, c);
+        c = mfma_16x16x32_f8(u32x2_t{kf[2], kf[3]}, u32x2_t{qf[t][2], qf[t][3]}, c);
+      } else {
+        c = mfma_16x16x32(kf, qf[t], c);
+      }
     }
     s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
   }
@@ -536,7 +572,7 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
   }
   float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                    fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-  mx = max_over_groups(mx) * a.scale_log2;
+  mx = max_over_groups(mx) * sl;
   // Lazy rescale: the reference max m moves only when a row's tile max exceeds it by
   // more than 8 (log2 units), so P <= 2^8 in between and O^T/l are rescaled rarely. This
   // is exact: O and l share the reference, and the output is O / l.
@@ -554,13 +590,54 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
   for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      p[pb][i] = __builtin_amdgcn_exp2f(fmaf(s[pb][i], a.scale_log2, -m));
+      p[pb][i] = __builtin_amdgcn_exp2f(fmaf(s[pb][i], sl, -m));
       ps += p[pb][i];
     }
   l += ps;
   const u32x4_t pk = {pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
                       pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
-  pv_accumulate<D>(stage + G::KBYTES, pk, acc, lane);
+  if constexpr (F8)
+    pv_accumulate_f8<D>(stage + G::KBYTES, pk, acc, lane);
+  else
+    pv_accumulate<D>(stage + G::KBYTES, pk, acc, lane);
+}
+
+// pv_accumulate for e4m3 V in the F8 stage layout: one ds_read_b64_tr_b8 per 16-channel
+// block gives lane (n, g) V[pos(g, j)][16 db + n] for j < 8 (pos(g, j) = 4 g + j, then
+// 16 + 4 g + j - 4: the positions of its P^T values). Within a 16-lane group the read
+// hands lane s, in slot j, byte s % 8 of the 8 bytes lane 2 j + s / 8 addressed, so lane
+// s addresses row pos(g, s / 2) at channels 16 db + 8 (s % 2). The e4m3 values are exact
+// in bf16.
+template <int D>
+__device__ __forceinline__ void pv_accumulate_f8(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
+                                                 int lane) {
+  using G = Geo<D, true>;
+  const int n = lane & 15, g = lane >> 4;
+  const int j = n >> 1;
+  const int r = j < 4 ? 4 * g + j : 12 + 4 * g + j;  // pos(g, j)
+  const uint32_t sw16 = 16u * (uint32_t)((r / G::R256) % G::LPR);
+  typedef __attribute__((address_space(3))) const char lds_char_t;
+  const uint32_t base = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + (r / G::RPB) * G::VPITCH + (r % G::RPB) * G::RB +
+                                                             8 * (n & 1));
+  u32x2_t w[G::DB];
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db)
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(w[db]) : "v"(base + (sw16 ^ (16u * db))));
+  static_assert(G::DB == 8 || G::DB == 4, "head_dim 128 or 64");
+  if constexpr (G::DB == 8) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]));
+  }
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db) {
+    const auto a0 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][0], false), a1 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][0], true);
+    const auto a2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][1], false), a3 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][1], true);
+    const u32x4_t vf = {pack_bf16x2(a0[0], a0[1]), pack_bf16x2(a1[0], a1[1]), pack_bf16x2(a2[0], a2[1]),
+                        pack_bf16x2(a3[0], a3[1])};
+    acc[db] = mfma_16x16x32(vf, pk, acc[db]);
+  }
 }
 
 // O^T += V^T P^T for one tile: pk holds this lane's bf16 P^T values (row n, positions
@@ -676,6 +753,99 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, con
   }
 }
 
+// The query pass of an fp8 call: the packed rows are e4m3 (row-major, D bytes each) with
+// a score scale per row, the query descale times the key descale of the row's (sequence,
+// KV head). q_fp8: the caller's rows are e4m3 with their descale; otherwise the bf16 rows
+// (after the optional prologue) are quantized as flashmap/sglang/model.py:167-169 does:
+// scale = max(amax, 1e-12) / 448 with amax over every token row of the row's query head
+// in its sequence, q / scale rounded to nearest even (q_len is a multiple of 16, so a
+// 16-row block holds one head; a head spanning several blocks has their rows re-read).
+// One wavefront per 16-row block, lane (n, g) holding channels 32 t + 8 g .. + 7.
+template <int D>
+__global__ __launch_bounds__(256) void pack_queries_f8_kernel(const AttnArgs a) {
+  constexpr int KT = D / 32;
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();  // (unit, row block)
+  const int64_t units = (int64_t)a.batch * a.ups;
+  if (blk >= units * a.nrb) return;  // wave-uniform; no barrier follows
+  const int64_t unit = blk / a.nrb;
+  const int rb = (int)(blk - unit * a.nrb);
+  const int b = (int)(unit / a.ups);
+  const int ul = (int)(unit - (int64_t)b * a.ups);
+  const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
+  const int r = rb * 16 + n;
+  const int R = rg * 16 * a.nrb + r;
+  const int gq = R / a.q_len, tq = R - gq * a.q_len;
+  const int qrows = q_rows_of(a, b);
+  const bool valid = gq < a.group && tq < qrows;
+  const int64_t head = (int64_t)h * a.group + (gq < a.group ? gq : 0);
+  const int64_t dix = (int64_t)b * a.d_sb + (int64_t)h * a.d_sh;
+  auto row_src = [&](int t_) {  // element offset of token t_ of this sequence, head `head`
+    return (a.cu_q ? (int64_t)(a.cu_q[b] + t_) * a.q_st : (int64_t)b * a.q_sb + (int64_t)t_ * a.q_st) +
+           head * a.q_sh;
+  };
+  u32x2_t q8[KT];
+  float rs;
+  if (a.q_fp8) {
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(a.q) + row_src(valid ? tq : 0) + 8 * g;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) q8[t] = valid ? *reinterpret_cast<const u32x2_t *>(src + 32 * t) : u32x2_t{0, 0};
+    rs = a.qd ? a.qd[dix] : 1.f;
+  } else {
+    auto load_row = [&](int t_, bool ok, u32x4_t (&x)[KT]) {  // every lane calls it (the norm crosses lanes)
+      const uint16_t *src = a.q + row_src(ok ? t_ : 0) + 8 * g;
+#pragma unroll
+      for (int t = 0; t < KT; ++t) x[t] = ok ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
+      if (a.qn_w != nullptr) {
+        const int64_t tok = q_token_index(a, b, ok ? t_ : 0);
+        const int64_t rr = clamp_row(a.rope, ok ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
+        norm_rope_row<D>(x, a.qn_w, a.eps, a.rope, rr, g);
+      }
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+        if (!ok) x[t] = u32x4_t{0, 0, 0, 0};
+    };
+    auto amax_of = [&](const u32x4_t (&x)[KT]) {
+      float mx = 0.f;
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fmaxf(fabsf(bf16_lo(x[t][q])), fabsf(bf16_hi(x[t][q]))));
+      return mx;
+    };
+    u32x4_t qf[KT];
+    load_row(tq, valid, qf);
+    float mx = amax_of(qf);
+    const int tq0 = tq - n;  // first token row of this block (all of head gq)
+    for (int k = 0; k < a.q_len; k += 16) {  // the head's other blocks
+      if (k == tq0) continue;
+      u32x4_t x[KT];
+      load_row(k + n, gq < a.group && k + n < qrows, x);
+      mx = fmaxf(mx, amax_of(x));
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = max_over_groups(mx);
+    const float scale = __fdiv_rn(fmaxf(mx, 1e-12f), 448.f);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[2 * q] = __fdiv_rn(bf16_lo(qf[t][q]), scale);
+        v[2 * q + 1] = __fdiv_rn(bf16_hi(qf[t][q]), scale);
+      }
+      q8[t] = u32x2_t{pack_e4m3x4(v[0], v[1], v[2], v[3]), pack_e4m3x4(v[4], v[5], v[6], v[7])};
+    }
+    rs = scale;
+  }
+  rs *= a.kd ? a.kd[dix] : 1.f;
+  uint8_t *dst = reinterpret_cast<uint8_t *>(const_cast<uint16_t *>(a.qp)) + (unit * 16 * a.nrb + r) * D + 8 * g;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) *reinterpret_cast<u32x2_t *>(dst + 32 * t) = valid ? q8[t] : u32x2_t{0, 0};
+  if (g == 0) a.q_rs[unit * 16 * a.nrb + r] = valid ? rs : 0.f;
+}
+
 // A segment's partial for this wavefront's 16 rows: O = acc * inv as fp16 of O / scale,
 // scale = the row's largest |O| (so every value is within [-1, 1] and keeps 11
 // significant bits wherever the row's magnitude lies). h[db] holds channels
@@ -751,7 +921,8 @@ __device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArg
       bool isk;
       load_slot<D>(i, lane, row, coff, isk, dst);
       const int j = j0 + (row < last ? row : last);
-      *reinterpret_cast<u32x4_t *>(vs + (dst - G::KBYTES) + lane * 16) = load16(vb + (tok0 + j) * v.v_st + coff);
+      *reinterpret_cast<u32x4_t *>(vs + (dst - G::KBYTES) + lane * 16) =
+          load16(reinterpret_cast<const char *>(vb + (tok0 + j) * v.v_st) + coff);
     }
     f32x4_t s[2];
 #pragma unroll
@@ -911,14 +1082,14 @@ __device__ __forceinline__ void lds_publish() { asm volatile("s_waitcnt lgkmcnt(
 // tile hands stage i from the producer (its loads complete) to the consumers and stage
 // i-1 back (their reads of it done), and a partial written in iteration t to the
 // producer, who stores it in iteration t + 1.
-template <int LAYOUT, int W, int D>
+template <int LAYOUT, int W, int D, bool F8 = false>
 __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     const AttnArgs a, const int32_t *__restrict__ table, const int32_t *__restrict__ plan,
     const int32_t *__restrict__ seqlens) {
-  using G = Geo<D>;
+  using G = Geo<D, F8>;
   using O = OutSlot<D, W>;
-  constexpr int KT = D / 32;
-  constexpr int UNIT_Q = 16 * W * D * 2;  // bytes of a unit's packed query rows
+  constexpr int QF = G::KC;                // 16-byte query fragments per lane
+  constexpr int UNIT_Q = 16 * W * G::RB;   // bytes of a unit's packed query rows
   constexpr bool IDS = LAYOUT != CONTIG;  // page ids join the load stream
   constexpr int R = replicas(W);
   constexpr int S = STAGES;
@@ -975,12 +1146,12 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     for (int i = 0; i < G::NI; ++i) {
       int row, coff, dst;
       bool isk;
-      load_slot<D>(i, lane, row, coff, isk, dst);
-      loff[i] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + 2u * (uint32_t)coff;
+      load_slot<D, F8>(i, lane, row, coff, isk, dst);
+      loff[i] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + (uint32_t)coff;
     }
     Loader ld;  // next tile to load (i + S - 1)
     ld.c = cc;
-    if (ntiles > 0) loader_unit<LAYOUT>(a, ld);
+    if (ntiles > 0) loader_unit<LAYOUT, G::ES>(a, ld);
     Cursor ct = cc;  // paged layouts: next tile whose page ids are loaded
     Cursor pc = cc;  // the tile whose partial (if any) is stored next
     bool pc_prev_end = false;
@@ -1001,16 +1172,16 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     };
     if (IDS) {
       for (int j = 0; j < S && j < ntiles; ++j) {
-        issue_ids<LAYOUT, D>(a, table, ct, stage(j), lane);
+        issue_ids<LAYOUT, D, F8>(a, table, ct, stage(j), lane);
         if (j + 1 < ntiles) cursor_next(a, sm, ct);
       }
       wait_vm<0>();
     }
     for (int j = 0; j < S - 1 && j < ntiles; ++j) {
-      issue_kv<LAYOUT, D, 1>(a, ld, stage(j), 0, lane, loff);
-      if (j + 1 < ntiles) loader_advance<LAYOUT>(a, sm, ld);
+      issue_kv<LAYOUT, D, 1, F8>(a, ld, stage(j), 0, lane, loff);
+      if (j + 1 < ntiles) loader_advance<LAYOUT, G::ES>(a, sm, ld);
       if (IDS && j + S <= 2 * S - 3 && j + S < ntiles) {
-        issue_ids<LAYOUT, D>(a, table, ct, stage(j + S), lane);
+        issue_ids<LAYOUT, D, F8>(a, table, ct, stage(j + S), lane);
         cursor_next(a, sm, ct);
       }
     }
@@ -1040,11 +1211,11 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       if (i >= ntiles) continue;
       if (i + S - 1 < ntiles) {
         if (IDS && i + 2 * S - 2 < ntiles) {
-          issue_ids<LAYOUT, D>(a, table, ct, stage(i + 2 * S - 2), lane);
+          issue_ids<LAYOUT, D, F8>(a, table, ct, stage(i + 2 * S - 2), lane);
           cursor_next(a, sm, ct);
         }
-        issue_kv<LAYOUT, D, 1>(a, ld, stage(i + S - 1), 0, lane, loff);
-        if (i + S < ntiles) loader_advance<LAYOUT>(a, sm, ld);
+        issue_kv<LAYOUT, D, 1, F8>(a, ld, stage(i + S - 1), 0, lane, loff);
+        if (i + S < ntiles) loader_advance<LAYOUT, G::ES>(a, sm, ld);
       }
     }
     block_sync();
@@ -1055,8 +1226,11 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
 
   // ------------------------------------------------------------------- consumers
   typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
-  const char *qbase = reinterpret_cast<const char *>(a.qp) + ((wave * 16 + n) * D + 8 * g) * 2;
+  const char *qbase = reinterpret_cast<const char *>(a.qp) + (wave * 16 + n) * G::RB + 16 * g;
   auto qsrc = [&](int u) { return qbase + (uint64_t)(uint32_t)u * UNIT_Q; };
+  // F8: the rows' score scales (query descale x key descale), loaded with the rows.
+  typedef __attribute__((address_space(1))) const float g_float_t;
+  auto qscale = [&](int u) { return *(g_float_t *)(a.q_rs + (int64_t)u * (16 * W) + wave * 16 + n); };
   // Query rows of the next unit are loaded into qn as soon as the current unit's are
   // taken (the first unit's before the producer's first loads are queued ahead of
   // them), so their latency hides behind a whole unit. The next unit on the line is
@@ -1064,10 +1238,12 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   // the unit starts.
   const int units = a.batch * a.ups;
   int qn_unit = -1;
-  u32x4_t qn[KT], qf[KT];
+  u32x4_t qn[QF], qf[QF];
+  float rsn = 1.f, sl = a.scale_log2;
   if (ntiles > 0) {
 #pragma unroll
-    for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
+    for (int t = 0; t < QF; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
+    if (F8) rsn = qscale(cc.u);
     qn_unit = cc.u;
   }
   f32x4_t acc[G::DB];
@@ -1079,17 +1255,20 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     if (i == 0 || cc.lt == 0) {  // a segment starts: its query rows
       if (qn_unit == cc.u) {
 #pragma unroll
-        for (int t = 0; t < KT; ++t) qf[t] = qn[t];
+        for (int t = 0; t < QF; ++t) qf[t] = qn[t];
+        if (F8) sl = a.scale_log2 * rsn;
       } else {
 #pragma unroll
-        for (int t = 0; t < KT; ++t) qf[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
+        for (int t = 0; t < QF; ++t) qf[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
+        if (F8) sl = a.scale_log2 * qscale(cc.u);
       }
 #pragma unroll
-      for (int t = 0; t < KT; ++t) asm volatile("" : "+v"(qf[t]));
+      for (int t = 0; t < QF; ++t) asm volatile("" : "+v"(qf[t]));
       qn_unit = -1;
       if (cc.u + 1 < units && cc.lt + ntiles - i > cc.tiles) {  // the share reaches unit u + 1
 #pragma unroll
-        for (int t = 0; t < KT; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u + 1) + 64 * t);
+        for (int t = 0; t < QF; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u + 1) + 64 * t);
+        if (F8) rsn = qscale(cc.u + 1);
         qn_unit = cc.u + 1;
       }
 #pragma unroll
@@ -1097,7 +1276,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       m = -INFINITY;
       l = 0.f;
     }
-    compute_tile<D>(a, stage(i), qf, acc, m, l, cc.lt * TILE, cc.L, lane);
+    compute_tile<D, F8>(a, stage(i), qf, sl, acc, m, l, cc.lt * TILE, cc.L, lane);
     const bool end = cc.lt == cc.tiles - 1 || i == ntiles - 1;
     if (end) {  // the segment ends: its partial
       const float lt_sum = sum_over_groups(l);
@@ -1193,7 +1372,8 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
   const int gq = R / a.q_len, tq = R - gq * a.q_len;
   if (gq >= a.group || tq >= qlen_b) return;
   RowMerge mg;
-  merge_partials<D>(a, unit, b, ul, r, c, a.v_scale, mg);
+  merge_partials<D>(a, unit, b, ul, r, c, a.vd ? a.v_scale * a.vd[(int64_t)b * a.d_sb + (int64_t)h * a.d_sh] : a.v_scale,
+                    mg);
   if (a.tail) {  // the verify tokens' partial
     typedef __attribute__((ext_vector_type(2))) float f32x2_t;
     const int64_t row = ((int64_t)a.batch * a.ups + a.num_shares + unit) * rows + r;
@@ -1245,29 +1425,34 @@ __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restri
 
 typedef void (*AttnKernel)(const AttnArgs, const int32_t *, const int32_t *, const int32_t *);
 
-template <int LAYOUT, int D>
+template <int LAYOUT, int D, bool F8>
 static AttnKernel pick_kernel(int w) {
   switch (w) {
-    case 1: return attn_fwd_kernel<LAYOUT, 1, D>;
-    case 2: return attn_fwd_kernel<LAYOUT, 2, D>;
-    case 3: return attn_fwd_kernel<LAYOUT, 3, D>;
-    case 4: return attn_fwd_kernel<LAYOUT, 4, D>;
-    case 5: return attn_fwd_kernel<LAYOUT, 5, D>;
-    case 6: return attn_fwd_kernel<LAYOUT, 6, D>;
-    case 7: return attn_fwd_kernel<LAYOUT, 7, D>;
-    default: return attn_fwd_kernel<LAYOUT, 8, D>;
+    case 1: return attn_fwd_kernel<LAYOUT, 1, D, F8>;
+    case 2: return attn_fwd_kernel<LAYOUT, 2, D, F8>;
+    case 3: return attn_fwd_kernel<LAYOUT, 3, D, F8>;
+    case 4: return attn_fwd_kernel<LAYOUT, 4, D, F8>;
+    case 5: return attn_fwd_kernel<LAYOUT, 5, D, F8>;
+    case 6: return attn_fwd_kernel<LAYOUT, 6, D, F8>;
+    case 7: return attn_fwd_kernel<LAYOUT, 7, D, F8>;
+    default: return attn_fwd_kernel<LAYOUT, 8, D, F8>;
   }
 }
 
-static AttnKernel select_kernel(int layout, int d, int w) {
-  if (d == 128) {
-    if (layout == CONTIG) return pick_kernel<CONTIG, 128>(w);
-    if (layout == PAGED16) return pick_kernel<PAGED16, 128>(w);
-    return pick_kernel<PAGED, 128>(w);
+// F8 (e4m3 K/V): the paged layouts only.
+static AttnKernel select_kernel(int layout, int d, int w, bool f8 = false) {
+  if (f8) {
+    if (d == 128) return layout == PAGED16 ? pick_kernel<PAGED16, 128, true>(w) : pick_kernel<PAGED, 128, true>(w);
+    return layout == PAGED16 ? pick_kernel<PAGED16, 64, true>(w) : pick_kernel<PAGED, 64, true>(w);
   }
-  if (layout == CONTIG) return pick_kernel<CONTIG, 64>(w);
-  if (layout == PAGED16) return pick_kernel<PAGED16, 64>(w);
-  return pick_kernel<PAGED, 64>(w);
+  if (d == 128) {
+    if (layout == CONTIG) return pick_kernel<CONTIG, 128, false>(w);
+    if (layout == PAGED16) return pick_kernel<PAGED16, 128, false>(w);
+    return pick_kernel<PAGED, 128, false>(w);
+  }
+  if (layout == CONTIG) return pick_kernel<CONTIG, 64, false>(w);
+  if (layout == PAGED16) return pick_kernel<PAGED16, 64, false>(w);
+  return pick_kernel<PAGED, 64, false>(w);
 }
 
 struct RowPlan {
@@ -1310,19 +1495,19 @@ struct Sizing {
   RowPlan rp;
   int num_wg;      // workgroups of the persistent grid
   int num_shares;  // num_wg * replicas
-  size_t plan_off, q_off, lse_off, o_off, bytes;
+  size_t plan_off, q_off, rs_off, lse_off, o_off, bytes;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// tail: a verify call (one more partial slot per unit, for its verify tokens).
+// tail: a verify call (one more partial slot per unit, for its verify tokens). f8: e4m3 K/V.
 static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int max_k,
-                  bool need_plan, Sizing *sz, bool tail = false) {
+                  bool need_plan, Sizing *sz, bool tail = false, bool f8 = false) {
   DeviceInfo info;
   int rc = device_info(&info);
   if (rc != FM_OK) return rc;
   sz->rp = row_plan(hq / hkv, q_len);
-  AttnKernel k = select_kernel(layout, d, sz->rp.nrb);
+  AttnKernel k = select_kernel(layout, d, sz->rp.nrb, f8);
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + TILE - 1) / TILE);
   const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
@@ -1343,6 +1528,8 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   if (need_plan) off = align256(off + sizeof(int32_t) * ((size_t)batch + 1));
   sz->q_off = off;
   off = align256(off + sizeof(uint16_t) * units * rows * d);
+  sz->rs_off = off;  // fp8 calls: score scale per packed row
+  off = align256(off + sizeof(float) * units * rows);
   sz->lse_off = off;
   off = align256(off + 2 * sizeof(float) * slots * rows);
   sz->o_off = off;
@@ -1382,28 +1569,35 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   FM_REQUIRE(c.q_sb % 8 == 0 && c.q_st % 8 == 0 && c.q_sh % 8 == 0 && c.o_sb % 8 == 0 &&
                  c.o_st % 8 == 0 && c.o_sh % 8 == 0,
              "query/output strides must be multiples of 8 elements");
-  FM_REQUIRE(a.u.k_s0 % 8 == 0 && a.u.k_s1 % 8 == 0 && a.k_s2 % 8 == 0 && a.u.v_s0 % 8 == 0 &&
-                 a.u.v_s1 % 8 == 0 && a.v_s2 % 8 == 0,
-             "key/value strides must be multiples of 8 elements");
+  const int es = a.f8 ? 1 : 2;  // bytes per K/V element
+  const int64_t kv_mult = 16 / es;  // the loads are 16-byte aligned
+  FM_REQUIRE(a.u.k_s0 % kv_mult == 0 && a.u.k_s1 % kv_mult == 0 && a.k_s2 % kv_mult == 0 &&
+                 a.u.v_s0 % kv_mult == 0 && a.u.v_s1 % kv_mult == 0 && a.v_s2 % kv_mult == 0,
+             "key/value strides must be multiples of %d elements", (int)kv_mult);
+  if (a.f8) {
+    if (layout == CONTIG) return fail(FM_ERR_UNSUPPORTED, "fp8 K/V needs a paged layout");
+    if (!a.q_fp8 && c.q_len % 16 != 0)
+      return fail(FM_ERR_UNSUPPORTED, "per-head query quantization needs max_seqlen_q %% 16 == 0 (got %d)", c.q_len);
+  }
   if (c.qn_w) FM_REQUIRE(c.rope_cos && c.rope_sin, "the query prologue needs the rotary table");
   // The kernels form per-tile addresses with 32-bit byte strides.
   if (a.k_s2 < 0 || a.v_s2 < 0 || a.k_s2 >= (1ll << 27) || a.v_s2 >= (1ll << 27))
     return fail(FM_ERR_UNSUPPORTED, "position strides must lie in [0, 2^27) elements");
-  a.k_tok_b = (uint32_t)(2 * a.k_s2);
-  a.v_tok_b = (uint32_t)(2 * a.v_s2);
+  a.k_tok_b = (uint32_t)(es * a.k_s2);
+  a.v_tok_b = (uint32_t)(es * a.v_s2);
   if (layout != CONTIG) {
     if (a.u.k_s0 < 0 || a.u.v_s0 < 0 || a.u.k_s0 >= (1ll << 31) || a.u.v_s0 >= (1ll << 31) ||
         (int64_t)a.page_size * (a.k_s2 > a.v_s2 ? a.k_s2 : a.v_s2) >= (1ll << 31))
       return fail(FM_ERR_UNSUPPORTED, "page strides must lie in [0, 2^31) elements");
-    a.k_page_b = (uint32_t)(2 * a.u.k_s0);
-    a.v_page_b = (uint32_t)(2 * a.u.v_s0);
+    a.k_page_b = (uint32_t)(es * a.u.k_s0);
+    a.v_page_b = (uint32_t)(es * a.u.v_s0);
     a.page_mask = (uint32_t)(a.page_size - 1);
     a.col_last = (uint32_t)(a.table_width - 1 < 0x7fffffffll ? a.table_width - 1 : 0x7fffffffll);
     a.page_last = (uint32_t)(a.num_pages - 1 < 0xffffffffll ? a.num_pages - 1 : 0xffffffffll);
   }
   const bool need_plan = a.seqlens != nullptr && c.plan == nullptr;
   Sizing sz;
-  int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr);
+  int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, a.f8 != 0);
   if (rc != FM_OK) return rc;
   if (c.ws == nullptr || c.ws_bytes < sz.bytes)
     return fail(FM_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", c.ws_bytes, sz.bytes);
@@ -1433,6 +1627,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   if (!a.tail) a.v_scale = 1.f;
   char *ws = (char *)c.ws;
   a.qp = (const uint16_t *)(ws + sz.q_off);
+  a.q_rs = (float *)(ws + sz.rs_off);
   a.part_lse = (float *)(ws + sz.lse_off);
   a.part_o = (uint16_t *)(ws + sz.o_off);
   if (a.seqlens != nullptr) {
@@ -1450,7 +1645,11 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   const int64_t qblocks = (units * sz.rp.nrb + 3) / 4;
   const VerifyArgs nov{};
-  if (vf != nullptr && c.d == 128)
+  if (a.f8 && c.d == 128)
+    pack_queries_f8_kernel<128><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
+  else if (a.f8)
+    pack_queries_f8_kernel<64><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
+  else if (vf != nullptr && c.d == 128)
     pack_queries_kernel<128, true><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, *vf);
   else if (vf != nullptr)
     pack_queries_kernel<64, true><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, *vf);
@@ -1459,7 +1658,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   else
     pack_queries_kernel<64, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
   FM_CHECK_HIP(hipGetLastError());
-  AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb);
+  AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb, a.f8 != 0);
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
@@ -1507,10 +1706,11 @@ extern "C" size_t fm_attn_workspace_bytes(int32_t batch, int32_t max_seqlen_q, i
   // with room for an in-call plan.
   size_t bytes = 0;
   int rc = FM_OK;
-  for (int layout = CONTIG; layout <= PAGED && rc == FM_OK; ++layout) {
+  for (int v = 0; v < 5 && rc == FM_OK; ++v) {  // the three layouts, then the two fp8 ones
+    const int layout = v < 3 ? v : v - 2;
     Sizing sz;
     rc = sizing(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, max_seqlen_k,
-                true, &sz);
+                true, &sz, false, v >= 3);
     if (rc == FM_OK && sz.bytes > bytes) bytes = sz.bytes;
   }
   if (device != prev) hipSetDevice(prev);
@@ -1536,8 +1736,8 @@ extern "C" int fm_block_attn_contig(
              q_norm_weight, rope_cos, rope_sin, rope_row_stride, rope_pair_stride, rope_rows,
              q_positions, eps, plan, workspace, workspace_bytes, (hipStream_t)stream};
   AttnArgs a{};
-  a.u.k = (const uint16_t *)k;
-  a.u.v = (const uint16_t *)v;
+  a.u.k = (const char *)k;
+  a.u.v = (const char *)v;
   a.u.k_s0 = k_stride_batch, a.u.k_s1 = k_stride_head, a.k_s2 = k_stride_pos;
   a.u.v_s0 = v_stride_batch, a.u.v_s1 = v_stride_head, a.v_s2 = v_stride_pos;
   // An empty cache: every sequence attends to nothing (zeros), whatever seqlens_k says.
@@ -1545,6 +1745,47 @@ extern "C" int fm_block_attn_contig(
   a.uniform_len = kv_len;
   a.u.pos_cap = kv_len;
   return run_attention(c, CONTIG, a);
+}
+
+// The vLLM cache view (layout PAGED16 for power-of-two pages of >= 16 positions).
+static int setup_paged(AttnArgs &a, int &layout, const void *kv_cache, int64_t num_blocks, int64_t stride_block,
+                       int64_t stride_head, int64_t stride_token, int64_t v_offset, int32_t page_size,
+                       const int32_t *block_table, int64_t block_table_stride, int64_t block_table_width,
+                       const int32_t *seqused_k, int es) {
+  FM_REQUIRE(kv_cache && block_table && seqused_k, "NULL cache/block table/seqused_k");
+  FM_REQUIRE(page_size > 0 && num_blocks > 0 && block_table_width > 0, "bad page geometry");
+  FM_REQUIRE(v_offset % (16 / es) == 0, "v_offset must be a multiple of %d elements", 16 / es);
+  const bool pow2 = (page_size & (page_size - 1)) == 0;
+  layout = (pow2 && page_size % 16 == 0) ? PAGED16 : PAGED;
+  a.u.k = (const char *)kv_cache;
+  a.u.v = (const char *)kv_cache + es * v_offset;
+  a.u.k_s0 = stride_block, a.u.k_s1 = stride_head, a.k_s2 = stride_token;
+  a.u.v_s0 = stride_block, a.u.v_s1 = stride_head, a.v_s2 = stride_token;
+  a.table = block_table;
+  a.u.table_stride = block_table_stride;
+  a.table_width = block_table_width;
+  a.num_pages = num_blocks;
+  a.page_size = page_size;
+  a.page_shift = pow2 ? __builtin_ctz((unsigned)page_size) : 0;
+  a.seqlens = seqused_k;
+  return FM_OK;
+}
+
+// The fp8 fields of a call: queries e4m3 (q_fp8) or bf16 to quantize, descales
+// (3, batch, kv heads) at [kind * s_kind + b * s_batch + h * s_head] or NULL (all 1).
+static int setup_fp8(AttnArgs &a, const CommonIn &c, int32_t q_fp8, const float *descales, int64_t s_kind,
+                     int64_t s_batch, int64_t s_head) {
+  FM_REQUIRE(!(q_fp8 && c.qn_w), "the query prologue needs bf16 queries");
+  a.f8 = 1;
+  a.q_fp8 = q_fp8 ? 1 : 0;
+  if (descales != nullptr) {
+    a.qd = q_fp8 ? descales : nullptr;
+    a.kd = descales + s_kind;
+    a.vd = descales + 2 * s_kind;
+    a.d_sb = s_batch;
+    a.d_sh = s_head;
+  }
+  return FM_OK;
 }
 
 extern "C" int fm_block_attn_paged(
@@ -1559,29 +1800,16 @@ extern "C" int fm_block_attn_paged(
     int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
     const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
     size_t workspace_bytes, void *stream) {
-  FM_REQUIRE(kv_cache && block_table && seqused_k, "NULL cache/block table/seqused_k");
-  FM_REQUIRE(page_size > 0 && num_blocks > 0 && block_table_width > 0, "bad page geometry");
-  FM_REQUIRE(v_offset % 8 == 0, "v_offset must be a multiple of 8 elements");
-  const bool pow2 = (page_size & (page_size - 1)) == 0;
-  const int layout = (pow2 && page_size % 16 == 0) ? PAGED16 : PAGED;
   CommonIn c{q, q_stride_batch, q_stride_token, q_stride_head, out, out_stride_batch,
              out_stride_token, out_stride_head, cu_seqlens_q, batch, max_seqlen_q, max_seqlen_k,
              num_q_heads, num_kv_heads, head_dim, softmax_scale, q_norm_weight, rope_cos,
              rope_sin, rope_row_stride, rope_pair_stride, rope_rows, q_positions, eps, plan,
              workspace, workspace_bytes, (hipStream_t)stream};
   AttnArgs a{};
-  a.u.k = (const uint16_t *)kv_cache;
-  a.u.v = (const uint16_t *)kv_cache + v_offset;
-  a.u.k_s0 = stride_block, a.u.k_s1 = stride_head, a.k_s2 = stride_token;
-  a.u.v_s0 = stride_block, a.u.v_s1 = stride_head, a.v_s2 = stride_token;
-  a.table = block_table;
-  a.u.table_stride = block_table_stride;
-  a.table_width = block_table_width;
-  a.num_pages = num_blocks;
-  a.page_size = page_size;
-  a.page_shift = pow2 ? __builtin_ctz((unsigned)page_size) : 0;
-  a.seqlens = seqused_k;
-  return run_attention(c, layout, a);
+  int layout = 0;
+  const int rc = setup_paged(a, layout, kv_cache, num_blocks, stride_block, stride_head, stride_token, v_offset,
+                             page_size, block_table, block_table_stride, block_table_width, seqused_k, 2);
+  return rc != FM_OK ? rc : run_attention(c, layout, a);
 }
 
 extern "C" int fm_block_attn_token_paged(
@@ -1604,8 +1832,8 @@ extern "C" int fm_block_attn_token_paged(
              rope_sin, rope_row_stride, rope_pair_stride, rope_rows, q_positions, eps, plan,
              workspace, workspace_bytes, (hipStream_t)stream};
   AttnArgs a{};
-  a.u.k = (const uint16_t *)key_buffer;
-  a.u.v = (const uint16_t *)value_buffer;
+  a.u.k = (const char *)key_buffer;
+  a.u.v = (const char *)value_buffer;
   a.u.k_s0 = k_stride_slot, a.u.k_s1 = k_stride_head, a.k_s2 = 0;
   a.u.v_s0 = v_stride_slot, a.u.v_s1 = v_stride_head, a.v_s2 = 0;
   a.table = page_table;
@@ -1671,8 +1899,8 @@ extern "C" int fm_verify_attention(
              num_kv_heads, head_dim, sm_scale * k_scale, nullptr, nullptr, nullptr, 0, 0, 0, nullptr,
              0.f, nullptr, workspace, workspace_bytes, (hipStream_t)stream};
   AttnArgs a{};
-  a.u.k = (const uint16_t *)key_buffer;
-  a.u.v = (const uint16_t *)value_buffer;
+  a.u.k = (const char *)key_buffer;
+  a.u.v = (const char *)value_buffer;
   a.u.k_s0 = k_stride_slot, a.u.k_s1 = k_stride_head, a.k_s2 = 0;
   a.u.v_s0 = v_stride_slot, a.u.v_s1 = v_stride_head, a.v_s2 = 0;
   a.table = (const int32_t *)kv_indices;
@@ -1689,4 +1917,65 @@ extern "C" int fm_verify_attention(
                 v_ext_stride_token, v_ext_stride_head, custom_mask, mask_indptr, mask_mode,
                 sm_scale * 1.4426950408889634f};
   return run_attention(c, PAGED, a, &vf);
+}
+
+extern "C" int fm_block_attn_paged_fp8(
+    const void *q, int32_t q_fp8, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *kv_cache, int64_t num_blocks, int64_t stride_block,
+    int64_t stride_head, int64_t stride_token, int64_t v_offset, int32_t page_size,
+    const int32_t *block_table, int64_t block_table_stride, int64_t block_table_width,
+    const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+    const float *descales, int64_t descale_stride_kind, int64_t descale_stride_batch,
+    int64_t descale_stride_head, const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows, const int64_t *q_positions,
+    float eps, const int32_t *plan, void *workspace, size_t workspace_bytes, void *stream) {
+  CommonIn c{q, q_stride_batch, q_stride_token, q_stride_head, out, out_stride_batch,
+             out_stride_token, out_stride_head, cu_seqlens_q, batch, max_seqlen_q, max_seqlen_k,
+             num_q_heads, num_kv_heads, head_dim, softmax_scale, q_norm_weight, rope_cos,
+             rope_sin, rope_row_stride, rope_pair_stride, rope_rows, q_positions, eps, plan,
+             workspace, workspace_bytes, (hipStream_t)stream};
+  AttnArgs a{};
+  int layout = 0;
+  int rc = setup_paged(a, layout, kv_cache, num_blocks, stride_block, stride_head, stride_token, v_offset,
+                       page_size, block_table, block_table_stride, block_table_width, seqused_k, 1);
+  if (rc == FM_OK)
+    rc = setup_fp8(a, c, q_fp8, descales, descale_stride_kind, descale_stride_batch, descale_stride_head);
+  return rc != FM_OK ? rc : run_attention(c, layout, a);
+}
+
+extern "C" int fm_block_attn_token_paged_fp8(
+    const void *q, int32_t q_fp8, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *key_buffer, const void *value_buffer, int64_t pool_size,
+    int64_t k_stride_slot, int64_t k_stride_head, int64_t v_stride_slot, int64_t v_stride_head,
+    const int32_t *page_table, int64_t page_table_stride, int64_t page_table_width,
+    const int32_t *cache_seqlens, int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+    const float *descales, int64_t descale_stride_kind, int64_t descale_stride_batch,
+    int64_t descale_stride_head, const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows, const int64_t *q_positions,
+    float eps, const int32_t *plan, void *workspace, size_t workspace_bytes, void *stream) {
+  FM_REQUIRE(key_buffer && value_buffer && page_table && cache_seqlens, "NULL pool/page table/seqlens");
+  FM_REQUIRE(pool_size > 0 && page_table_width > 0, "bad pool geometry");
+  CommonIn c{q, q_stride_batch, q_stride_token, q_stride_head, out, out_stride_batch,
+             out_stride_token, out_stride_head, cu_seqlens_q, batch, max_seqlen_q, max_seqlen_k,
+             num_q_heads, num_kv_heads, head_dim, softmax_scale, q_norm_weight, rope_cos,
+             rope_sin, rope_row_stride, rope_pair_stride, rope_rows, q_positions, eps, plan,
+             workspace, workspace_bytes, (hipStream_t)stream};
+  AttnArgs a{};
+  a.u.k = (const char *)key_buffer;
+  a.u.v = (const char *)value_buffer;
+  a.u.k_s0 = k_stride_slot, a.u.k_s1 = k_stride_head, a.k_s2 = 0;
+  a.u.v_s0 = v_stride_slot, a.u.v_s1 = v_stride_head, a.v_s2 = 0;
+  a.table = page_table;
+  a.u.table_stride = page_table_stride;
+  a.table_width = page_table_width;
+  a.num_pages = pool_size;
+  a.page_size = 1;
+  a.page_shift = 0;
+  a.seqlens = cache_seqlens;
+  const int rc = setup_fp8(a, c, q_fp8, descales, descale_stride_kind, descale_stride_batch, descale_stride_head);
+  return rc != FM_OK ? rc : run_attention(c, PAGED, a);
 }

@@ -55,6 +55,13 @@ __device__ __forceinline__ f32x4_t mfma_16x16x16(u32x2_t a, u32x2_t b, f32x4_t c
                                                     __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
 }
 
+// D(16x16 f32) += A(16x32 e4m3) * B(32x16 e4m3) (gfx950: OCP e4m3); 8 bytes per lane each,
+// lane (row / column n, g) holding reduction indices 8 g .. 8 g + 7.
+__device__ __forceinline__ f32x4_t mfma_16x16x32_f8(u32x2_t a, u32x2_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0,
+                                                     0, 0);
+}
+
 // Cross-lane pairs with gfx950's v_permlane16_swap / v_permlane32_swap: each returns,
 // in every lane l, the two values {v[l], v[l ^ 16]} (resp. {v[l], v[l ^ 32]}) in some
 // order, so a symmetric operation of the pair gives the same bits in both lanes.
@@ -206,6 +213,56 @@ __device__ __forceinline__ void norm_rope_apply(u32x4_t (&x)[D / 32], const Prol
       x[t][q] = pack_bf16x2(e2, o2);
     }
   }
+}
+
+// The same RMSNorm + RoPE with the rotated values left in fp32 (the fp8 writers divide
+// them by the cache's scale and quantize them directly): y[t][2q], y[t][2q + 1] = the
+// rotated pair 16 t + 4 g + q. SGL: the normed value is rounded once, bf16((x r) w), as
+// sglang's fp8 pool writer computes it (flashmap/sglang/kernels.py:326-329); otherwise
+// bf16(x bf16(w r)) as above (flashmap/vllm/kernels.py:276-290).
+template <int D, bool SGL>
+__device__ __forceinline__ void norm_rope_f32(const u32x4_t (&x)[D / 32], const PrologueOps<D> &ops, float eps,
+                                              float (&y)[D / 32][8]) {
+  constexpr int KT = D / 32;
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float e = bf16_lo(x[t][q]), o = bf16_hi(x[t][q]);
+      ss = __fadd_rn(ss, __fmul_rn(e, e));
+      ss = __fadd_rn(ss, __fmul_rn(o, o));
+    }
+  }
+  ss = sum_over_groups(ss);
+  const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float e, o;
+      if constexpr (SGL) {
+        e = round_bf16(__fmul_rn(__fmul_rn(bf16_lo(x[t][q]), r), ops.w[t][2 * q]));
+        o = round_bf16(__fmul_rn(__fmul_rn(bf16_hi(x[t][q]), r), ops.w[t][2 * q + 1]));
+      } else {
+        e = round_bf16(__fmul_rn(bf16_lo(x[t][q]), round_bf16(__fmul_rn(ops.w[t][2 * q], r))));
+        o = round_bf16(__fmul_rn(bf16_hi(x[t][q]), round_bf16(__fmul_rn(ops.w[t][2 * q + 1], r))));
+      }
+      const float c = ops.c[t][q], s = ops.s[t][q];
+      y[t][2 * q] = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s));
+      y[t][2 * q + 1] = __fadd_rn(__fmul_rn(o, c), __fmul_rn(e, s));
+    }
+  }
+}
+
+// OCP e4m3 (the fp8 KV caches): round to nearest even, saturated to the largest finite
+// value +-448 (the conversion the reference's writers use). Byte j of the result holds
+// v[j].
+__device__ __forceinline__ uint32_t pack_e4m3x4(float v0, float v1, float v2, float v3) {
+  auto sat = [](float v) { return v > 448.f ? 448.f : (v < -448.f ? -448.f : v); };  // NaN stays NaN
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(sat(v0), sat(v1), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(sat(v2), sat(v3), w, true);
+  return (uint32_t)w;
 }
 
 template <int D>

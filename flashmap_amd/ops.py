@@ -22,7 +22,9 @@ __all__ = [
     "attention_plan",
     "block_attention_contig",
     "block_attention_paged",
+    "block_attention_paged_fp8",
     "block_attention_token_paged",
+    "block_attention_token_paged_fp8",
     "block_self_attention",
     "rms_norm_rope",
     "rope_from_cat",
@@ -32,7 +34,9 @@ __all__ = [
     "verify_workspace_bytes",
     "workspace_for",
     "write_context_kv",
+    "write_context_kv_fp8",
     "write_context_kv_pool",
+    "write_context_kv_pool_fp8",
 ]
 
 
@@ -369,6 +373,125 @@ def block_attention_token_paged(
     return out
 
 
+# ------------------------------------------------------------------- fp8 (e4m3) KV
+
+
+def _fp8_query(query: torch.Tensor, out: torch.Tensor | None, varlen: bool):
+    """(query, out, query strides, out strides, q_fp8) of an fp8-cache call: e4m3 (or
+    uint8) queries are passed as bytes, bf16 ones are quantized in the call."""
+    if query.element_size() == 1:
+        ok = query.stride(-1) == 1 and query.data_ptr() % 16 == 0 and all(st % 8 == 0 for st in query.stride()[:-1])
+        q = query if ok else query.contiguous()
+        if out is None:
+            out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        if varlen:
+            qs, os_ = [0, q.stride(0), q.stride(1)], [0, out.stride(0), out.stride(1)]
+        else:
+            qs, os_ = [q.stride(0), q.stride(1), q.stride(2)], [out.stride(0), out.stride(1), out.stride(2)]
+        return q, out, qs, os_, 1
+    q, out, qs, os_ = _q_out(query, out, varlen)
+    return q, out, qs, os_, 0
+
+
+def _descale_args(descales: torch.Tensor | None) -> list:
+    """(pointer, kind, batch, head strides) of FlashAttention-style descales (3, batch,
+    kv_heads) float32 (expanded views allowed)."""
+    if descales is None:
+        return [None, 0, 0, 0]
+    d = descales if descales.dtype == torch.float32 else descales.float()
+    return [d.data_ptr(), d.stride(0), d.stride(1), d.stride(2)]
+
+
+def block_attention_paged_fp8(
+    query: torch.Tensor,
+    kv_cache: torch.Tensor,
+    cu_seqlens_q: torch.Tensor | None,
+    seqused_k: torch.Tensor,
+    block_table: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    descales: torch.Tensor | None = None,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`block_attention_paged` onto an e4m3 cache ``(num_blocks, Hkv, page, 2D)``
+    (one byte per element): ``query`` e4m3 (quantized by the caller, ``descales[0]`` its
+    descale) or bf16 (quantized per (request, query head) in the call); ``descales (3,
+    requests, Hkv)`` = query, key, value descales (flashmap/vllm/model.py:93-134, 863-873).
+    Returns bf16."""
+    _check_cuda(query, kv_cache, cu_seqlens_q, seqused_k, block_table, descales)
+    _fp8_cache(kv_cache, "kv_cache")
+    tokens, hq, d = query.shape
+    num_blocks, hkv, page, two_d = kv_cache.shape
+    if two_d != 2 * d or kv_cache.stride(-1) != 1:
+        raise ValueError(f"kv_cache must be (blocks, heads, page, 2 * {d}) with unit channel stride")
+    batch = seqused_k.shape[0]
+    query, out, qs, os_, q_fp8 = _fp8_query(query, out, varlen=True)
+    if batch == 0 or tokens == 0:
+        return out
+    cu = None if cu_seqlens_q is None else _i32(cu_seqlens_q)
+    if cu is None:
+        qs[0], os_[0] = max_seqlen_q * qs[1], max_seqlen_q * os_[1]
+    bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(-1) == 1) else _i32(block_table)
+    sk = _i32(seqused_k)
+    ws = workspace_for(batch, max_seqlen_q, hq, hkv, d, max_seqlen_k, query.device)
+    call(
+        "fm_block_attn_paged_fp8",
+        query.data_ptr(), q_fp8, *qs, out.data_ptr(), *os_, _ptr(cu),
+        kv_cache.data_ptr(), num_blocks, kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), d, page,
+        bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
+        hq, hkv, d, float(softmax_scale), *_descale_args(descales),
+        *(prologue.args() if prologue else _NO_PROLOGUE),
+        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
+def block_attention_token_paged_fp8(
+    query: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    page_table: torch.Tensor,
+    softmax_scale: float | None = None,
+    descales: torch.Tensor | None = None,
+    max_seqlen_k: int | None = None,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`block_attention_token_paged` onto e4m3 pools: ``query (bs, q_len, Hq, D)``
+    bf16 is quantized per (request, query head) with scale amax / 448 and every operand
+    descaled, as flashmap_sglang::paged_cross_attention_fp8 does
+    (flashmap/sglang/model.py:154-181); an e4m3 ``query`` takes ``descales[0]``."""
+    _check_cuda(query, key_buffer, value_buffer, cache_seqlens, page_table, descales)
+    _fp8_cache(key_buffer, "key_buffer")
+    _fp8_cache(value_buffer, "value_buffer")
+    batch, q_len, hq, d = query.shape
+    pool, hkv, _ = key_buffer.shape
+    query, out, qs, os_, q_fp8 = _fp8_query(query, out, varlen=False)
+    if batch == 0 or q_len == 0:
+        return out
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
+    pt = page_table if (page_table.dtype == torch.int32 and page_table.stride(-1) == 1) else _i32(page_table)
+    sl = _i32(cache_seqlens)
+    max_k = pt.shape[1] if max_seqlen_k is None else max_seqlen_k
+    ws = workspace_for(batch, q_len, hq, hkv, d, max_k, query.device)
+    call(
+        "fm_block_attn_token_paged_fp8",
+        query.data_ptr(), q_fp8, *qs, out.data_ptr(), *os_, None,
+        key_buffer.data_ptr(), value_buffer.data_ptr(), pool,
+        key_buffer.stride(0), key_buffer.stride(1), value_buffer.stride(0), value_buffer.stride(1),
+        pt.data_ptr(), pt.stride(0), pt.shape[1], sl.data_ptr(), batch, q_len, max_k,
+        hq, hkv, d, float(scale), *_descale_args(descales),
+        *(prologue.args() if prologue else _NO_PROLOGUE),
+        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
 # ------------------------------------------------------------------ verify attention
 
 _VERIFY_WS_BYTES: dict[tuple, int] = {}
@@ -582,6 +705,87 @@ def write_context_kv_pool(
         kv.data_ptr(), tokens, num_layers, heads, head_dim, _i64(meta).data_ptr(),
         _f32(k_norm_weights).data_ptr(), *rope.args(), _i64(positions).data_ptr(), _i64(locs).data_ptr(),
         _ptr(cl), int(locs_row_width or 0), float(eps), _stream(kv),
+    )
+
+
+def _fp8_cache(t: torch.Tensor, name: str) -> None:
+    if t.element_size() != 1:
+        raise TypeError(f"{name} must be an fp8 (e4m3) or uint8 tensor, got {t.dtype}")
+
+
+def write_context_kv_fp8(
+    kv: torch.Tensor,
+    positions: torch.Tensor,
+    slots: torch.Tensor,
+    k_norm: torch.Tensor,
+    rope: Rope,
+    cache_ptrs: torch.Tensor,
+    cache_strides: tuple[int, int, int, int],
+    block_size: int,
+    eps: float,
+    scales: torch.Tensor,
+    heads_per_cache: int | None = None,
+) -> None:
+    """:func:`write_context_kv` into e4m3 caches (one byte per element, strides in
+    elements) with per-layer ``scales (layers, 2)`` (key, value); see
+    fm_write_context_kv_fp8 (flashmap/vllm/kernels.py:292-299)."""
+    _check_cuda(kv, positions, slots, k_norm, cache_ptrs, scales)
+    if kv.dtype != torch.bfloat16:
+        raise TypeError(f"kv must be bfloat16, got {kv.dtype}")
+    kv = kv.contiguous()
+    tokens, layers, _, heads, d = kv.shape
+    if tokens == 0:
+        return
+    hpc = heads_per_cache or heads
+    if cache_ptrs.numel() * hpc < layers * heads:
+        raise ValueError(f"{cache_ptrs.numel()} caches of {hpc} heads cannot hold {layers} x {heads} heads")
+    if scales.numel() < 2 * layers:
+        raise ValueError(f"scales must hold (layers, 2) = {2 * layers} values, got {scales.numel()}")
+    sb, sh, st, voff = cache_strides
+    kn, sc = _f32(k_norm), _f32(scales)
+    call(
+        "fm_write_context_kv_fp8",
+        kv.data_ptr(), tokens, layers, heads, d, _i64(positions).data_ptr(), _i64(slots).data_ptr(),
+        kn.data_ptr(), *rope.args(), _i64(cache_ptrs).data_ptr(), cache_ptrs.numel(), hpc,
+        sb, sh, st, voff, block_size, sc.data_ptr(), float(eps), _stream(kv),
+    )
+
+
+def write_context_kv_pool_fp8(
+    kv: torch.Tensor,
+    meta: torch.Tensor,
+    k_norm_weights: torch.Tensor,
+    rope: Rope,
+    positions: torch.Tensor,
+    locs: torch.Tensor,
+    num_layers: int,
+    kv_size: int,
+    head_dim: int,
+    eps: float,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    commit_lens: torch.Tensor | None = None,
+    locs_row_width: int | None = None,
+) -> None:
+    """:func:`write_context_kv_pool` into e4m3 pools with static scales and the pool
+    writer's norm rounding; see fm_write_context_kv_pool_fp8
+    (flashmap/sglang/kernels.py:283-357)."""
+    _check_cuda(kv, meta, k_norm_weights, positions, locs, commit_lens)
+    if kv.dtype != torch.bfloat16:
+        raise TypeError(f"kv must be bfloat16, got {kv.dtype}")
+    kv = kv.contiguous()
+    tokens = kv.shape[0]
+    if tokens == 0:
+        return
+    heads = kv_size // head_dim
+    if kv.numel() != tokens * num_layers * 2 * kv_size:
+        raise ValueError("kv must be (tokens, layers * 2 * kv_size)")
+    cl = None if commit_lens is None else _i32(commit_lens)
+    call(
+        "fm_write_context_kv_pool_fp8",
+        kv.data_ptr(), tokens, num_layers, heads, head_dim, _i64(meta).data_ptr(),
+        _f32(k_norm_weights).data_ptr(), *rope.args(), _i64(positions).data_ptr(), _i64(locs).data_ptr(),
+        _ptr(cl), int(locs_row_width or 0), float(k_scale), float(v_scale), float(eps), _stream(kv),
     )
 
 

@@ -83,8 +83,8 @@ int fm_rms_norm_rope(const void *x, void *out, int64_t tokens, int32_t heads, in
  * G x q_len rows packed contiguously in the workspace, with the prologue applied), the
  * split-KV attention and the fp32 log-sum-exp combine that writes `out`. Split-KV:
  * the context of all sequences is cut into equal shares over a persistent grid (one
- * share per workgroup); every (unit, share) segment leaves an fp32 partial that the
- * combine merges. `plan` is fm_attn_plan's output for this step (it depends only on
+ * share per workgroup); every (unit, share) segment leaves a partial (fp16 values
+ * with a per-row scale, fp32 log-sum-exp) that the combine merges. `plan` is fm_attn_plan's output for this step (it depends only on
  * the context lengths, so every layer of a step may share it); NULL plans inside the
  * call, in the workspace. `workspace` must hold fm_attn_workspace_bytes(...) bytes for
  * the same arguments (packed queries, partials, plan); it is scratch that concurrent
@@ -160,6 +160,49 @@ int fm_block_attn_token_paged(
     int64_t page_table_width, const int32_t *cache_seqlens, int32_t batch, int32_t max_seqlen_q,
     int32_t max_seqlen_k, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
     float softmax_scale, const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* FP8 (OCP e4m3) K/V: the same calls onto caches holding one byte per element (strides
+ * in elements = bytes, multiples of 16), with FlashAttention's descale convention:
+ * descales (3, batch, num_kv_heads) float32 at [kind * descale_stride_kind + b *
+ * descale_stride_batch + h * descale_stride_head], kind 0 = query, 1 = key, 2 = value
+ * (NULL: all 1). Scores are (q8 . k8) * q_descale * k_descale * softmax_scale, values
+ * v8 * v_descale; P is rounded to bf16 before P.V, the output to bf16 once.
+ * q_fp8 != 0: q holds e4m3 bytes (the caller quantized them; strides in bytes), no
+ * prologue. q_fp8 == 0: q is bf16 (with the optional prologue) and the call quantizes
+ * each (sequence, query head)'s rows with scale max(amax |q|, 1e-12) / 448, as
+ * flashmap/sglang/model.py:167-169 does (the query part of descales is not read;
+ * max_seqlen_q must be a multiple of 16). Workspace: fm_attn_workspace_bytes.
+ * fm_block_attn_paged_fp8 replaces flashmap_vllm::paged_cross_attention with descales
+ * (flashmap/vllm/model.py:93-134, 863-873); fm_block_attn_token_paged_fp8 replaces
+ * flashmap_sglang::paged_cross_attention_fp8 (flashmap/sglang/model.py:154-181).
+ */
+int fm_block_attn_paged_fp8(
+    const void *q, int32_t q_fp8, int64_t q_stride_batch, int64_t q_stride_token,
+    int64_t q_stride_head, void *out, int64_t out_stride_batch, int64_t out_stride_token,
+    int64_t out_stride_head, const int32_t *cu_seqlens_q, const void *kv_cache, int64_t num_blocks,
+    int64_t stride_block, int64_t stride_head, int64_t stride_token, int64_t v_offset,
+    int32_t page_size, const int32_t *block_table, int64_t block_table_stride,
+    int64_t block_table_width, const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q,
+    int32_t max_seqlen_k, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, const float *descales, int64_t descale_stride_kind,
+    int64_t descale_stride_batch, int64_t descale_stride_head, const float *q_norm_weight,
+    const float *rope_cos, const float *rope_sin, int64_t rope_row_stride,
+    int64_t rope_pair_stride, int64_t rope_rows, const int64_t *q_positions, float eps,
+    const int32_t *plan, void *workspace, size_t workspace_bytes, void *stream);
+int fm_block_attn_token_paged_fp8(
+    const void *q, int32_t q_fp8, int64_t q_stride_batch, int64_t q_stride_token,
+    int64_t q_stride_head, void *out, int64_t out_stride_batch, int64_t out_stride_token,
+    int64_t out_stride_head, const int32_t *cu_seqlens_q, const void *key_buffer,
+    const void *value_buffer, int64_t pool_size, int64_t k_stride_slot, int64_t k_stride_head,
+    int64_t v_stride_slot, int64_t v_stride_head, const int32_t *page_table,
+    int64_t page_table_stride, int64_t page_table_width, const int32_t *cache_seqlens,
+    int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, float softmax_scale, const float *descales,
+    int64_t descale_stride_kind, int64_t descale_stride_batch, int64_t descale_stride_head,
+    const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
     int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
     const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
     size_t workspace_bytes, void *stream);
@@ -258,6 +301,34 @@ int fm_write_context_kv_pool(const void *kv, int64_t tokens, int32_t layers, int
                              int64_t rope_rows, const int64_t *positions, const int64_t *locs,
                              const int32_t *commit_lens, int64_t locs_row_width, float eps,
                              void *stream);
+
+/* FP8 (OCP e4m3, one byte per element) versions of the two writers. Keys are k-normed
+ * and rotated as above but kept in fp32 through the rotation; keys and values are then
+ * divided by the cache's scale, rounded to nearest even and saturated to +-448.
+ * fm_write_context_kv_fp8: scales (layers, 2) float32 device array of per-layer (key,
+ * value) scales; strides in elements (= bytes). Replaces write_context_kv for fp8 caches
+ * (flashmap/vllm/kernels.py:292-299, 311-364).
+ * fm_write_context_kv_pool_fp8: one (k_scale, v_scale) pair, and the pool writer's norm
+ * rounding bf16(x * r * w) (r = 1 / sqrt(mean(x^2) + eps)); meta strides in elements.
+ * Replaces kv_norm_rope_write_fp8 (flashmap/sglang/kernels.py:283-357).
+ */
+int fm_write_context_kv_fp8(const void *kv, int64_t tokens, int32_t layers, int32_t heads,
+                            int32_t head_dim, const int64_t *positions, const int64_t *slots,
+                            const float *k_norm_weight, const float *rope_cos,
+                            const float *rope_sin, int64_t rope_row_stride,
+                            int64_t rope_pair_stride, int64_t rope_rows,
+                            const int64_t *cache_ptrs, int32_t num_caches,
+                            int32_t heads_per_cache, int64_t stride_block, int64_t stride_head,
+                            int64_t stride_token, int64_t v_offset, int32_t page_size,
+                            const float *scales, float eps, void *stream);
+int fm_write_context_kv_pool_fp8(const void *kv, int64_t tokens, int32_t layers, int32_t heads,
+                                 int32_t head_dim, const int64_t *meta,
+                                 const float *k_norm_weight, const float *rope_cos,
+                                 const float *rope_sin, int64_t rope_row_stride,
+                                 int64_t rope_pair_stride, int64_t rope_rows,
+                                 const int64_t *positions, const int64_t *locs,
+                                 const int32_t *commit_lens, int64_t locs_row_width,
+                                 float k_scale, float v_scale, float eps, void *stream);
 
 /* ---------------------------------------------------------------------------------
  * Measurement hook. No reference counterpart: it lets a benchmark time the main

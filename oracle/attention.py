@@ -336,6 +336,157 @@ def write_context_kv_vllm(kv, positions, slots, k_norm, cos_sin, caches, block_s
                 caches[c][page, s, tok, d:] = kv[t, l, 1, h]
 
 
+# ------------------------------------------------------------------- fp8 (e4m3) KV
+
+
+E4M3_MAX = 448.0
+
+
+def to_e4m3(x: torch.Tensor) -> torch.Tensor:
+    """Round to OCP e4m3 (nearest even) saturating at +-448, the conversion the
+    reference's Triton writers use for fp8 caches (flashmap/vllm/kernels.py:292-299,
+    flashmap/sglang/kernels.py:330-335). Returns a float8_e4m3fn tensor.
+    Pinned by: nearest-code brute force over all 256 codes with ties to even
+    (test_oracle_fp8)."""
+    return x.float().clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+
+
+def rotate_f32(y: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Interleaved-pair RoPE of ``y`` in float32 without the final rounding (the fp8
+    writers quantize the rotated keys directly: flashmap/vllm/kernels.py:287-296,
+    flashmap/sglang/kernels.py:330-331)."""
+    e, o = y[..., 0::2].float(), y[..., 1::2].float()
+    out = torch.empty(y.shape, dtype=torch.float32)
+    out[..., 0::2] = e * cos - o * sin
+    out[..., 1::2] = o * cos + e * sin
+    return out
+
+
+def norm_sglang_fp8(k: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """The fp8 pool writer's RMSNorm: ``bf16((x * r) * w)`` with ``r = 1 / sqrt(mean(x^2)
+    + eps)``, one rounding (flashmap/sglang/kernels.py:325-329), where the bf16 paths
+    round the scale first (:func:`rms_norm`). Pinned by: float64 restatement; differs
+    from rms_norm on some inputs (test_oracle_fp8)."""
+    kf = k.float()
+    inv = 1.0 / torch.sqrt((kf * kf).mean(dim=-1, keepdim=True) + eps)
+    return (kf * inv * weight.float()).to(torch.bfloat16)
+
+
+def write_context_kv_vllm_fp8(kv, positions, slots, k_norm, cos_sin, caches, block_size, eps, scales,
+                              heads_per_cache=None):
+    """vLLM ``write_context_kv`` for e4m3 caches (flashmap/vllm/kernels.py:276-299):
+    keys k-normed (bf16 rounding as :func:`rms_norm`), rotated in float32, divided by the
+    layer's key scale; values divided by its value scale; both :func:`to_e4m3`.
+    ``caches`` are float8_e4m3fn ``(num_blocks, HPC, page, 2D)`` tensors, updated in place;
+    ``scales (L, 2)``. Pinned by: dequantized round trip == project_keys / v within half
+    an e4m3 step (test_oracle_fp8)."""
+    tokens, layers, _, heads, d = kv.shape
+    hpc = heads_per_cache or heads
+    rows = cos_sin[positions.long()]
+    cos, sin = rows[..., 0][:, None, :], rows[..., 1][:, None, :]
+    for t in range(tokens):
+        slot = int(slots[t])
+        if slot < 0:
+            continue
+        page, tok = divmod(slot, block_size)
+        for l in range(layers):
+            ks, vs = float(scales[l, 0]), float(scales[l, 1])
+            keys = rotate_f32(rms_norm(kv[t, l, 0], k_norm[l], eps), cos[t], sin[t])
+            for h in range(heads):
+                g = l * heads + h
+                c, s_ = divmod(g, hpc)
+                caches[c][page, s_, tok, :d] = to_e4m3(keys[h] / ks)
+                caches[c][page, s_, tok, d:] = to_e4m3(kv[t, l, 1, h].float() / vs)
+
+
+def write_context_kv_pool_fp8(kv, k_bufs, v_bufs, k_norm, cos_sin_cat, positions, locs, num_layers, kv_size,
+                              head_dim, eps, k_scale=1.0, v_scale=1.0, commit_lens=None, locs_row_width=None):
+    """``kv_norm_rope_write_fp8`` (flashmap/sglang/kernels.py:283-357): as
+    :func:`write_context_kv_pool` into float8_e4m3fn pools, keys normed by
+    :func:`norm_sglang_fp8`, rotated in float32, both divided by their static scale
+    and :func:`to_e4m3`. Pinned by: dequantized round trip (test_oracle_fp8)."""
+    heads = kv_size // head_dim
+    half = head_dim // 2
+    rows = cos_sin_cat[positions.long()]
+    cos, sin = rows[:, None, :half], rows[:, None, half:]
+    for t in range(kv.shape[0]):
+        loc = int(locs[t])
+        if loc < 0:
+            continue
+        if commit_lens is not None and t % locs_row_width >= int(commit_lens[t // locs_row_width]):
+            continue
+        for l in range(num_layers):
+            base = l * 2 * kv_size
+            k = kv[t, base:base + kv_size].view(heads, head_dim)
+            v = kv[t, base + kv_size:base + 2 * kv_size].view(heads, head_dim)
+            keys = rotate_f32(norm_sglang_fp8(k, k_norm[l], eps), cos[t], sin[t])
+            k_bufs[l][loc] = to_e4m3(keys / k_scale)
+            v_bufs[l][loc] = to_e4m3(v.float() / v_scale)
+
+
+def quantize_query_per_head(query: torch.Tensor):
+    """``query (bs, T, H, D)`` -> (e4m3 query, scale (bs, H)): scale = max(amax |q| over
+    (T, D), 1e-12) / 448, q8 = q / scale rounded to e4m3, as
+    flashmap_sglang::paged_cross_attention_fp8 quantizes (flashmap/sglang/model.py:167-169).
+    Pinned by: each head's largest |q| maps to 448; dequantized within half an e4m3 step
+    (test_oracle_fp8)."""
+    scale = query.float().abs().amax(dim=(1, 3)).clamp_min(1e-12) / 448.0
+    return (query.float() / scale[:, None, :, None]).to(torch.float8_e4m3fn), scale
+
+
+def block_attention_paged_vllm_fp8(query, kv_cache, cu_seqlens_q, seqused_k, block_table, scale, descales=None):
+    """a6 onto an e4m3 cache with FlashAttention's descales (flashmap/vllm/model.py:93-134,
+    863-873): ``query (tokens, Hq, D)`` e4m3, ``descales (3, requests, Hkv)`` (query, key,
+    value; None = 1); attention of the dequantized operands q8 q_d, k8 k_d, v8 v_d in
+    float32. Returns float32 (tokens, Hq, D). Pinned by: :func:`attention` (pinned) on
+    exactly dequantized e4m3 values (test_oracle_fp8)."""
+    tokens, hq, d = query.shape
+    hkv = kv_cache.shape[1]
+    g = hq // hkv
+    qf = query.float()
+    cache = kv_cache.float()
+    out = torch.zeros(tokens, hq, d)
+    bt = np.asarray(block_table)
+    for b in range(len(seqused_k)):
+        lo, hi = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+        n = int(seqused_k[b])
+        if n <= 0 or hi <= lo:
+            continue
+        k, v = gather_vllm(cache, bt, n, b)  # (Hkv, n, D)
+        q = qf[lo:hi].transpose(0, 1).clone()  # (Hq, T, D)
+        if descales is not None:
+            qd, kd, vd = (descales[i, b].float() for i in range(3))
+            q = q * qd.repeat_interleave(g)[:, None, None]
+            k = k * kd[:, None, None]
+            v = v * vd[:, None, None]
+        out[lo:hi] = attention(q, k, v, scale).transpose(0, 1)
+    return out
+
+
+def block_attention_token_paged_fp8(query, key_buffer, value_buffer, cache_seqlens, page_table, scale=None,
+                                    descales=None):
+    """a7 onto e4m3 pools as flashmap_sglang::paged_cross_attention_fp8 computes it
+    (flashmap/sglang/model.py:154-181): the bf16 ``query (bs, T, Hq, D)`` quantized by
+    :func:`quantize_query_per_head`, keys and values descaled by ``descales[1:]`` (None =
+    1, the pool written with scale 1), attention of the dequantized operands in float32.
+    Returns float32 (bs, T, Hq, D). Pinned by: composition of pinned parts (test_oracle_fp8)."""
+    q8, qs = quantize_query_per_head(query)
+    qd = q8.float() * qs[:, None, :, None]
+    kf, vf = key_buffer.float(), value_buffer.float()
+    out = torch.zeros(query.shape)
+    for b in range(query.shape[0]):
+        n = int(cache_seqlens[b])
+        if n <= 0:
+            continue
+        rows = torch.as_tensor(np.asarray(page_table)[b, :n]).long()
+        k, v = kf[rows].transpose(0, 1), vf[rows].transpose(0, 1)
+        if descales is not None:
+            k = k * descales[1, b].float()[:, None, None]
+            v = v * descales[2, b].float()[:, None, None]
+        out[b] = attention(qd[b].transpose(0, 1), k, v, scale).transpose(0, 1)
+    return out
+
+
 def write_context_kv_pool(kv, k_bufs, v_bufs, k_norm, cos_sin_cat, positions, locs, num_layers, kv_size,
                           head_dim, eps, commit_lens=None, locs_row_width=None):
     """SGLang pool write (fused_kv_norm_rope_write as flashmap/sglang/model.py:746-766
