@@ -78,10 +78,10 @@ def build_inputs(name: str, seed: int = 0):
                 q_pre=q_pre, kv_pre=kv_pre, positions=positions, slots=slots, lo=lo, hi=hi)
 
 
-def algorithmic_bytes(inp) -> dict:
+def algorithmic_bytes(inp, kv_bytes: int = 2) -> dict:
     lens, d, hq, hkv, k_rows, batch, page = (inp[k] for k in ("lens", "d", "hq", "hkv", "k_rows", "batch", "page"))
     sum_l = int(lens.sum())
-    kv = sum_l * hkv * d * 2 * 2
+    kv = sum_l * hkv * d * 2 * kv_bytes
     qo = 2 * batch * k_rows * hq * d * 2
     table = 4 * sum(math.ceil(int(n) / page) for n in lens)
     meta = 8 * batch
@@ -151,6 +151,13 @@ def cpu_baseline(inp, budget_s: float = 12.0) -> dict:
                   f"positions): fp32 oracle Q prologue + block-table gather + attention, scaled by positions",
     }
 
+
+# The drafter workloads onto an e4m3 (fp8) paged cache: name -> the bf16 workload whose
+# draw it shares. The cache is written by the fp8 context writer (scales 1); the queries
+# are bf16, normed and rotated and quantized per (sequence, head) inside the call.
+FP8_WORKLOADS = {
+    "c3-qwen3-8b-paged-b64-fp8": "c3-qwen3-8b-paged-b64",
+}
 
 # Target verify attention (SplitKVVerify's call): name -> (batch, hq, hkv, head_dim,
 # verify tokens, ctx lo, ctx hi, mask). Contexts as the drafter workloads draw them,
@@ -278,7 +285,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64", choices=sorted(WORKLOADS) + sorted(VERIFY_WORKLOADS))
+    ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64",
+                    choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", type=int, default=0,
@@ -305,18 +313,23 @@ def main() -> int:
     from flashmap_amd import _native, ops
     from oracle import attention as ref
 
-    inp = build_inputs(args.workload)
+    fp8 = args.workload in FP8_WORKLOADS
+    inp = build_inputs(FP8_WORKLOADS.get(args.workload, args.workload))
     batch, hq, hkv, d, k_rows, page = (inp[k] for k in ("batch", "hq", "hkv", "d", "k_rows", "page"))
     table = ref.rope_table(inp["hi"] + k_rows + 1, d, 1e6).to(dev)
     rope = ops.rope_from_table(table)
     w = torch.ones(d, device=dev)
     lens = inp["lens"].to(dev, torch.int32)
     bt = inp["bt"].to(dev)
-    cache = torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.bfloat16, device=dev)
+    cache = torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.uint8 if fp8 else torch.bfloat16, device=dev)
     ptrs = torch.tensor([cache.data_ptr()], dtype=torch.int64, device=dev)
-    ops.write_context_kv(inp["kv_pre"].to(dev), inp["positions"].to(dev), inp["slots"].to(dev),
-                         w[None].expand(1, d).contiguous(), rope, ptrs,
-                         (cache.stride(0), cache.stride(1), cache.stride(2), d), page, 1e-6)
+    writer_args = (inp["kv_pre"].to(dev), inp["positions"].to(dev), inp["slots"].to(dev),
+                   w[None].expand(1, d).contiguous(), rope, ptrs,
+                   (cache.stride(0), cache.stride(1), cache.stride(2), d), page, 1e-6)
+    if fp8:
+        ops.write_context_kv_fp8(*writer_args, torch.ones(1, 2, device=dev))
+    else:
+        ops.write_context_kv(*writer_args)
     q_pre = inp["q_pre"].to(dev)
     qpos = torch.cat([int(n) + torch.arange(k_rows) for n in inp["lens"]]).to(dev)
     cu = (torch.arange(batch + 1, dtype=torch.int32) * k_rows).to(dev)
@@ -326,8 +339,12 @@ def main() -> int:
     out = torch.empty_like(q_pre)
 
     def call():
-        ops.block_attention_paged(q_pre, cache, cu, lens, bt, k_rows, max_k, d ** -0.5,
-                                  prologue=pro, plan=plan, out=out)
+        if fp8:
+            ops.block_attention_paged_fp8(q_pre, cache, cu, lens, bt, k_rows, max_k, d ** -0.5,
+                                          prologue=pro, plan=plan, out=out)
+        else:
+            ops.block_attention_paged(q_pre, cache, cu, lens, bt, k_rows, max_k, d ** -0.5,
+                                      prologue=pro, plan=plan, out=out)
 
     for _ in range(args.warmup):
         call()
@@ -353,9 +370,9 @@ def main() -> int:
     lib.fm_profile_enable(0)
     kernel_ms = tot.value / max(cnt.value, 1)
 
-    ab = algorithmic_bytes(inp)
+    ab = algorithmic_bytes(inp, kv_bytes=1 if fp8 else 2)
     traffic = None
-    tfile = ROOT / "profiles" / f"attn_fwd_{args.workload.split('-', 1)[0]}_paged_b{batch}.traffic.json"
+    tfile = ROOT / "profiles" / f"attn_fwd_{args.workload.split('-', 1)[0]}_paged_b{batch}{'_fp8' if fp8 else ''}.traffic.json"
     if tfile.exists():
         rec = json.loads(tfile.read_text())
         if rec.get("workload") == args.workload:
@@ -373,7 +390,7 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "e4m3 K/V, bf16 q" if fp8 else "bf16",
         "data": "synthetic: seeded CPU draw (lengths, permuted block table, q, K/V), K k-normed and "
                 "rotated on the GPU by the context writer",
         "config": {
@@ -381,6 +398,7 @@ def main() -> int:
             "batch": batch, "q_heads": hq, "kv_heads": hkv, "head_dim": d, "block_queries": k_rows,
             "ctx_lo": inp["lo"], "ctx_hi": inp["hi"], "ctx_sum": ab["sum_l"], "page": page,
             "layout": "vllm paged (blocks, kv_heads, page, 2*head_dim)", "prologue": "fused",
+            "kv_dtype": "e4m3" if fp8 else "bf16",
         },
         "hbm_tbs": round(ab["total"] / (ms * 1e-3) / 1e12, 3),
         "kv_tbs": round(ab["kv"] / (ms * 1e-3) / 1e12, 3),

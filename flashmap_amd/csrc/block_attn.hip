@@ -51,7 +51,8 @@ namespace fm {
 
 constexpr int TILE = 32;    // context positions per tile
 constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
-constexpr int STAGES = 3;   // LDS ring depth (tiles)
+constexpr int STAGES = 3;     // LDS ring depth (tiles), bf16 K/V
+constexpr int STAGES_F8 = 6;  // e4m3 K/V: tiles of half the bytes, so twice the tiles in flight
 
 // Replicas per workgroup: R independent groups of W consumer wavefronts and one producer
 // wavefront, each streaming its own share through its own LDS ring, that meet at one
@@ -155,7 +156,8 @@ struct Geo {
   static constexpr int VBYTES = VBLKS * VPITCH;
   static constexpr int TBYTES = 128;           // page ids of the tile (generic paging)
   static constexpr int STAGE = KBYTES + VBYTES + TBYTES;
-  static constexpr int SMEM = STAGES * STAGE;
+  static constexpr int NS = F8 ? STAGES_F8 : STAGES;  // ring depth
+  static constexpr int SMEM = NS * STAGE;
 };
 
 __device__ __forceinline__ int64_t share_start(int64_t w, int64_t total, int64_t nw) {
@@ -551,14 +553,23 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
 #pragma unroll
   for (int pb = 0; pb < 2; ++pb) {
     f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (F8 && G::KC == 2) {  // head_dim 128: one 128-channel fp8 MFMA
+      const u32x4_t k0 = *reinterpret_cast<const u32x4_t *>(stage + (pb * 2) * 1024 + lane * 16);
+      const u32x4_t k1 = *reinterpret_cast<const u32x4_t *>(stage + (pb * 2 + 1) * 1024 + lane * 16);
+      const i32x8_t ka = {(int)k0[0], (int)k0[1], (int)k0[2], (int)k0[3], (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
+      const i32x8_t qb = {(int)qf[0][0], (int)qf[0][1], (int)qf[0][2], (int)qf[0][3],
+                          (int)qf[1][0], (int)qf[1][1], (int)qf[1][2], (int)qf[1][3]};
+      c = mfma_16x16x128_f8(ka, qb, c);
+    } else {
 #pragma unroll
-    for (int t = 0; t < G::KC; ++t) {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(stage + (pb * G::KC + t) * 1024 + lane * 16);
-      if constexpr (F8) {
-        c = mfma_16x16x32_f8(u32x2_t{kf[0], kf[1]}, u32x2_t{qf[t][0], qf[t][1]}, c);
-        c = mfma_16x16x32_f8(u32x2_t{kf[2], kf[3]}, u32x2_t{qf[t][2], qf[t][3]}, c);
-      } else {
-        c = mfma_16x16x32(kf, qf[t], c);
+      for (int t = 0; t < G::KC; ++t) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(stage + (pb * G::KC + t) * 1024 + lane * 16);
+        if constexpr (F8) {
+          c = mfma_16x16x32_f8(u32x2_t{kf[0], kf[1]}, u32x2_t{qf[t][0], qf[t][1]}, c);
+          c = mfma_16x16x32_f8(u32x2_t{kf[2], kf[3]}, u32x2_t{qf[t][2], qf[t][3]}, c);
+        } else {
+          c = mfma_16x16x32(kf, qf[t], c);
+        }
       }
     }
     s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
@@ -632,10 +643,8 @@ __device__ __forceinline__ void pv_accumulate_f8(const char *vbase, const u32x4_
   }
 #pragma unroll
   for (int db = 0; db < G::DB; ++db) {
-    const auto a0 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][0], false), a1 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][0], true);
-    const auto a2 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][1], false), a3 = __builtin_amdgcn_cvt_pk_f32_fp8(w[db][1], true);
-    const u32x4_t vf = {pack_bf16x2(a0[0], a0[1]), pack_bf16x2(a1[0], a1[1]), pack_bf16x2(a2[0], a2[1]),
-                        pack_bf16x2(a3[0], a3[1])};
+    const u32x4_t vf = {e4m3x2_to_bf16x2(w[db][0], false), e4m3x2_to_bf16x2(w[db][0], true),
+                        e4m3x2_to_bf16x2(w[db][1], false), e4m3x2_to_bf16x2(w[db][1], true)};
     acc[db] = mfma_16x16x32(vf, pk, acc[db]);
   }
 }
@@ -1092,7 +1101,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   constexpr int UNIT_Q = 16 * W * G::RB;   // bytes of a unit's packed query rows
   constexpr bool IDS = LAYOUT != CONTIG;  // page ids join the load stream
   constexpr int R = replicas(W);
-  constexpr int S = STAGES;
+  constexpr int S = G::NS;
   constexpr int RBYTES = G::SMEM + O::BYTES;  // per replica: the ring, then the out slot
   static_assert(S >= 3, "the wait schedule keeps one group between tiles");
   static_assert((S - 2) * G::NI + (S - 2) < 64, "vmcnt holds 6 bits");

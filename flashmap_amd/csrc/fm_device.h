@@ -62,6 +62,22 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32_f8(u32x2_t a, u32x2_t b, f32x4_
                                                      0, 0);
 }
 
+// D(16x16 f32) += A(16x128 e4m3) * B(128x16 e4m3) (v_mfma_scale_f32_16x16x128_f8f6f4, both
+// formats e4m3, unit block scales); 32 bytes per lane each. The reduction index's lane
+// layout only has to agree between A and B: a lane's 32 bytes of A and of B must hold
+// the same 32 channels in the same order.
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+__device__ __forceinline__ f32x4_t mfma_16x16x128_f8(const i32x8_t &a, const i32x8_t &b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0x7f7f7f7f, 0, 0x7f7f7f7f);
+}
+// Two e4m3 values (bytes 0, 1 of w, or 2, 3 with hi) as bf16x2, exactly.
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w, bool hi) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 b2_t;
+  const b2_t v = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                    : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Cross-lane pairs with gfx950's v_permlane16_swap / v_permlane32_swap: each returns,
 // in every lane l, the two values {v[l], v[l ^ 16]} (resp. {v[l], v[l ^ 32]}) in some
 // order, so a symmetric operation of the pair gives the same bits in both lanes.
