@@ -73,6 +73,51 @@ def paged_cross_attention(
                                            plan=plan)
 
 
+def paged_cross_attention_fp8(
+    query: torch.Tensor,
+    key_buffer: torch.Tensor,
+    value_buffer: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    page_table: torch.Tensor,
+    scheduler_metadata: torch.Tensor | None,
+) -> torch.Tensor:
+    """:func:`paged_cross_attention` onto an e4m3 pool written with scale 1: the bf16
+    query is quantized per (request, head) with scale amax / 448 and every operand
+    descaled (flashmap/sglang/model.py:154-181); returns the query's dtype."""
+    plan = scheduler_metadata
+    if plan is not None and (plan.dtype != torch.int32 or plan.numel() != cache_seqlens.shape[0] + 1):
+        raise ValueError("scheduler_metadata must be cross_attention_schedule(cache_seqlens) or None")
+    return ops.block_attention_token_paged_fp8(query, key_buffer, value_buffer, cache_seqlens, page_table,
+                                               plan=plan)
+
+
+def kv_norm_rope_write_fp8(
+    kv: torch.Tensor,
+    meta: torch.Tensor,
+    k_norm_weights: torch.Tensor,
+    cos_sin: torch.Tensor,
+    positions: torch.Tensor,
+    locs: torch.Tensor,
+    num_layers: int,
+    kv_size: int,
+    head_dim: int,
+    eps: float,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+    commit_lens: torch.Tensor | None = None,
+    locs_row_width: int | None = None,
+) -> None:
+    """:func:`fused_kv_norm_rope_write` (same arguments, interleaved RoPE) for e4m3 pools:
+    keys k-normed (one rounding, bf16(x r w)) and rotated, keys and values divided by
+    their static scale (flashmap/sglang/kernels.py:336-357)."""
+    if kv.shape[0] == 0:
+        return
+    ops.write_context_kv_pool_fp8(kv, meta, k_norm_weights, ops.rope_from_cat(cos_sin), positions, locs,
+                                  num_layers, kv_size, head_dim, eps, k_scale=k_scale, v_scale=v_scale,
+                                  commit_lens=commit_lens, locs_row_width=locs_row_width)
+
+
 def fused_kv_norm_rope_write(
     kv: torch.Tensor,
     meta: torch.Tensor,
@@ -120,10 +165,14 @@ def register(namespace: str = NAMESPACE) -> dict[str, object]:
     cross = lib.custom_op(f"{namespace}::paged_cross_attention", mutates_args=())(paged_cross_attention)
     cross.register_fake(lambda query, key_buffer, value_buffer, cache_seqlens, page_table, meta:
                         torch.empty_like(query))
+    cross8 = lib.custom_op(f"{namespace}::paged_cross_attention_fp8", mutates_args=())(paged_cross_attention_fp8)
+    cross8.register_fake(lambda query, key_buffer, value_buffer, cache_seqlens, page_table, meta:
+                         torch.empty_like(query))
     _OPS[namespace] = {"rms_norm_rope": norm, "block_self_attention": self_attn,
-                       "paged_cross_attention": cross}
+                       "paged_cross_attention": cross, "paged_cross_attention_fp8": cross8}
     return _OPS[namespace]
 
 
 __all__ = ["block_self_attention", "cross_attention_schedule", "fused_kv_norm_rope_write",
-           "paged_cross_attention", "register", "rms_norm_rope", "rope_freqs"]
+           "kv_norm_rope_write_fp8", "paged_cross_attention", "paged_cross_attention_fp8", "register",
+           "rms_norm_rope", "rope_freqs"]

@@ -82,11 +82,15 @@ def paged_cross_attention(
 ) -> torch.Tensor:
     """Non-causal attention of ``query (tokens, heads, head_dim)`` onto the first
     ``seqused_k`` cached positions of each request (vLLM's ``(blocks, kv_heads, page,
-    2 * head_dim)`` cache, K then V in each row). ``fa_version`` is accepted and
-    ignored."""
+    2 * head_dim)`` cache, K then V in each row). An fp8 cache takes an e4m3 ``query``
+    and ``descales (3, requests, kv_heads)`` for the query, keys and values
+    (flashmap/vllm/model.py:93-134). ``fa_version`` is accepted and ignored."""
     del fa_version
     if descales is not None:
-        raise NotImplementedError("fp8 KV caches are not supported by flashmap_amd yet")
+        return ops.block_attention_paged_fp8(
+            query, kv_cache, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k,
+            softmax_scale, descales=descales, plan=_plan(scheduler_metadata, seqused_k.shape[0]),
+        )
     return ops.block_attention_paged(
         query, kv_cache, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k,
         softmax_scale, plan=_plan(scheduler_metadata, seqused_k.shape[0]),
@@ -108,9 +112,13 @@ def write_context_kv(
 ) -> None:
     """Every layer's context keys (k-normed, rotated) and values of ``kv (tokens,
     layers, 2, heads, head_dim)`` written into the paged caches at ``slots`` (negative
-    slots skipped), heads in layer-major order, ``heads_per_cache`` per cache."""
+    slots skipped), heads in layer-major order, ``heads_per_cache`` per cache. With
+    ``scales (layers, 2)`` the caches are e4m3 and keys / values are divided by the
+    layer's scales (flashmap/vllm/kernels.py:292-299)."""
     if scales is not None:
-        raise NotImplementedError("fp8 KV caches are not supported by flashmap_amd yet")
+        ops.write_context_kv_fp8(kv, positions, slots, k_norm, ops.rope_from_table(cos_sin), cache_ptrs,
+                                 cache_strides, block_size, eps, scales, heads_per_cache)
+        return
     ops.write_context_kv(kv, positions, slots, k_norm, ops.rope_from_table(cos_sin), cache_ptrs,
                          cache_strides, block_size, eps, heads_per_cache)
 

@@ -130,3 +130,74 @@ def test_sglang_block_self_attention_op(dev, plugin_ops):
     got = s.block_self_attention(qkv.to(dev), qn.to(dev), kn.to(dev), freqs.to(dev), 1e-6)
     want = ref.block_self_attention(qkv, qn, kn, freqs[..., 0], freqs[..., 1], 1e-6)
     check_close(got, want)
+
+
+def test_vllm_fp8_write_then_paged_cross_attention(dev, plugin_ops):
+    """The fp8 flow of the vLLM plugin (flashmap/vllm/model.py:863-873): an e4m3 cache
+    written with per-layer scales, the query quantized by the caller with its static
+    scale, the attention op given descales (3, requests, heads)."""
+    v, _, fv, _ = plugin_ops
+    g = gen(21)
+    b, h, d, k_rows, page, eps = 4, 8, 128, 16, 16, 1e-6
+    lens = torch.tensor([33, 100, 7, 64])
+    bt, total = paged_layout(lens, page, g)
+    table = ref.rope_table(200, d, 1e6)
+    knorm = torch.rand(1, d, generator=g) + 0.5
+    toks = int(lens.sum())
+    kv = torch.randn(toks, 1, 2, h, d, generator=g).bfloat16()
+    pos = torch.cat([torch.arange(int(n)) for n in lens])
+    slots = torch.cat([bt[i, torch.arange(int(n)) // page].long() * page + torch.arange(int(n)) % page
+                       for i, n in enumerate(lens)])
+    scales = torch.tensor([[0.8, 1.25]])
+    cache = torch.zeros(total, h, page, 2 * d, dtype=torch.uint8, device=dev)
+    ptrs = torch.tensor([cache.data_ptr()], dtype=torch.int64, device=dev)
+    fv.write_context_kv(kv.to(dev), pos.to(dev), slots.to(dev), knorm.to(dev), table.to(dev), ptrs,
+                        (cache.stride(0), cache.stride(1), cache.stride(2), d), page, eps, scales=scales.to(dev))
+    q = torch.randn(b * k_rows, h, d, generator=g).bfloat16()
+    q_scale = 0.05
+    q8 = (q.float() / q_scale).to(torch.float8_e4m3fn)
+    descales = torch.stack([torch.tensor(q_scale), scales[0, 0], scales[0, 1]])[:, None, None].expand(3, b, h)
+    cu = (torch.arange(b + 1, dtype=torch.int32) * k_rows).to(dev)
+    sk = lens.to(dev, torch.int32)
+    out = v.paged_cross_attention(q8.to(dev), cache, cu, sk, bt.to(dev), fv.cross_attention_schedule(sk),
+                                  descales.to(dev), k_rows, 128, d ** -0.5, 3)
+    want_cache = torch.zeros(total, h, page, 2 * d, dtype=torch.float8_e4m3fn)
+    ref.write_context_kv_vllm_fp8(kv, pos, slots, knorm, table, [want_cache], page, eps, scales)
+    want = ref.block_attention_paged_vllm_fp8(q8, want_cache, cu.cpu(), lens, bt, d ** -0.5, descales.contiguous())
+    check_close(out, want)
+
+
+def test_sglang_fp8_pool_write_then_attention(dev, plugin_ops):
+    """kv_norm_rope_write_fp8 into e4m3 pools, then flashmap_sglang::paged_cross_attention_fp8
+    (flashmap/sglang/model.py:154-181, flashmap/sglang/kernels.py:336-357)."""
+    _, s, _, fs = plugin_ops
+    g = gen(22)
+    bs, k_rows, h, d, eps = 3, 16, 4, 128, 1e-6
+    lens = torch.tensor([50, 17, 90])
+    pool = int(lens.sum()) + 20
+    kv_size = h * d
+    toks = int(lens.sum())
+    kv = torch.randn(toks, 2 * kv_size, generator=g).bfloat16()
+    pos = torch.cat([torch.arange(int(n)) for n in lens])
+    locs = torch.randperm(pool, generator=g)[:toks].long()
+    knorm = torch.rand(1, d, generator=g) + 0.5
+    cat = ref.rope_cat_table(256, d, 1e6)
+    kb = torch.zeros(pool, h, d, dtype=torch.uint8, device=dev)
+    vb = torch.zeros(pool, h, d, dtype=torch.uint8, device=dev)
+    meta = torch.tensor([[kb.data_ptr(), vb.data_ptr(), kb.stride(0), vb.stride(0)]], dtype=torch.int64, device=dev)
+    fs.kv_norm_rope_write_fp8(kv.to(dev), meta, knorm.to(dev), cat.to(dev), pos.to(dev), locs.to(dev), 1, kv_size,
+                              d, eps)
+    pt = torch.zeros(bs, int(lens.max()), dtype=torch.int32)
+    o = 0
+    for i in range(bs):
+        pt[i, :int(lens[i])] = locs[o:o + int(lens[i])].int()
+        o += int(lens[i])
+    q = torch.randn(bs, k_rows, h, d, generator=g).bfloat16()
+    sl = lens.to(dev, torch.int32)
+    out = s.paged_cross_attention_fp8(q.to(dev), kb.view(torch.float8_e4m3fn), vb.view(torch.float8_e4m3fn), sl,
+                                      pt.to(dev), fs.cross_attention_schedule(sl))
+    wk = [torch.zeros(pool, h, d, dtype=torch.float8_e4m3fn)]
+    wv = [torch.zeros(pool, h, d, dtype=torch.float8_e4m3fn)]
+    ref.write_context_kv_pool_fp8(kv, wk, wv, knorm, cat, pos, locs, 1, kv_size, d, eps)
+    want = ref.block_attention_token_paged_fp8(q, wk[0], wv[0], lens, pt)
+    check_close(out.float(), want)

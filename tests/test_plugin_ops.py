@@ -53,16 +53,35 @@ def test_sglang_fake_shapes(ns):
     assert out.shape == q.shape
     x = _e(2, 16, 8, 128, dtype=torch.bfloat16)
     assert s.rms_norm_rope(x, _e(128), _e(2, 16, 64, 2), 1e-6).shape == x.shape
+    kb8 = _e(1000, 8, 128, dtype=torch.float8_e4m3fn)
+    out8 = s.paged_cross_attention_fp8(q, kb8, kb8, _e(8, dtype=torch.int32), _e(8, 300, dtype=torch.int32), None)
+    assert out8.shape == q.shape and out8.dtype == q.dtype
 
 
 def test_unsupported_variants_raise():
     q = torch.zeros(16, 4, 64, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
-        fv.paged_cross_attention(q, q, q, q, q, None, torch.ones(3, 1, 4), 16, 64, 0.125, 3)
-    with pytest.raises(NotImplementedError):
-        fv.write_context_kv(q, q, q, q, q, q, (1, 1, 1, 1), 16, 1e-6, scales=torch.ones(1, 2))
-    with pytest.raises(NotImplementedError):
         fs.fused_kv_norm_rope_write(q, q, q, q, q, q, 1, 256, 64, 1e-6, is_neox_style=True)
+
+
+def test_fp8_variants_route_to_the_kernels():
+    """The fp8 variants (vLLM descales / scales, SGLang's _fp8 ops) reach the fp8 kernel
+    wrappers, which refuse CPU tensors (no CPU fallback)."""
+    q8 = torch.zeros(16, 4, 64, dtype=torch.float8_e4m3fn)
+    cache8 = torch.zeros(2, 4, 16, 128, dtype=torch.uint8)
+    i32 = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        fv.paged_cross_attention(q8, cache8, i32, i32[:1], torch.zeros(1, 2, dtype=torch.int32), None,
+                                 torch.ones(3, 1, 4), 16, 64, 0.125, 3)
+    kv = torch.zeros(3, 1, 2, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        fv.write_context_kv(kv, torch.zeros(3, dtype=torch.long), torch.zeros(3, dtype=torch.long),
+                            torch.ones(1, 64), torch.zeros(8, 32, 2), torch.zeros(1, dtype=torch.long),
+                            (1, 1, 1, 1), 16, 1e-6, scales=torch.ones(1, 2))
+    qb = torch.zeros(1, 16, 4, 64, dtype=torch.bfloat16)
+    pool8 = torch.zeros(10, 4, 64, dtype=torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="GPU"):
+        fs.paged_cross_attention_fp8(qb, pool8, pool8, i32[:1], torch.zeros(1, 4, dtype=torch.int32), None)
 
 
 def test_rope_freqs_matches_oracle_table():
