@@ -49,10 +49,11 @@
 
 namespace fm {
 
-constexpr int TILE = 32;    // context positions per tile
+constexpr int TILE = 32;    // context positions per tile (bf16 K/V)
+constexpr int TILE_F8 = 64; // e4m3 K/V: the same bytes per tile as bf16
 constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
 constexpr int STAGES = 3;     // LDS ring depth (tiles), bf16 K/V
-constexpr int STAGES_F8 = 6;  // e4m3 K/V: tiles of half the bytes, so twice the tiles in flight
+constexpr int STAGES_F8 = 3;  // e4m3 K/V (tiles of TILE_F8 positions)
 
 // Replicas per workgroup: R independent groups of W consumer wavefronts and one producer
 // wavefront, each streaming its own share through its own LDS ring, that meet at one
@@ -141,20 +142,22 @@ struct AttnArgs {
 template <int D, bool F8 = false>
 struct Geo {
   static constexpr int ES = F8 ? 1 : 2;        // bytes per element
+  static constexpr int T = F8 ? TILE_F8 : TILE; // positions per tile
+  static constexpr int NH = T / 16;             // 16-row blocks (page halves) per tile
   static constexpr int RB = D * ES;            // bytes per row
   static constexpr int KT = D / 32;            // bf16 k-steps over head_dim
   static constexpr int KC = RB / 64;           // 64-byte slices of a row (K blocks per 16 rows)
   static constexpr int DB = D / 16;            // 16-channel blocks of O^T
-  static constexpr int KFRAGS = 2 * KC;        // 1 KB K blocks per tile
+  static constexpr int KFRAGS = NH * KC;       // 1 KB K blocks per tile
   static constexpr int LPR = RB / 16;          // 16-byte chunks per row
   static constexpr int RPB = 64 / LPR;         // V rows per 1 KB block
-  static constexpr int VBLKS = TILE / RPB;     // V blocks per tile
+  static constexpr int VBLKS = T / RPB;        // V blocks per tile
   static constexpr int VPITCH = F8 ? 1024 : 1024 + 32;  // bytes per V block (bf16: with pad)
   static constexpr int R256 = 256 / RB;        // FP8: rows per 256 bytes (the swizzle period)
   static constexpr int NI = KFRAGS + VBLKS;    // 16-byte LDS-DMA loads per lane per tile
   static constexpr int KBYTES = KFRAGS * 1024;
   static constexpr int VBYTES = VBLKS * VPITCH;
-  static constexpr int TBYTES = 128;           // page ids of the tile (generic paging)
+  static constexpr int TBYTES = 4 * T;         // page ids of the tile (generic paging)
   static constexpr int STAGE = KBYTES + VBYTES + TBYTES;
   static constexpr int NS = F8 ? STAGES_F8 : STAGES;  // ring depth
   static constexpr int SMEM = NS * STAGE;
@@ -390,14 +393,14 @@ __device__ __forceinline__ void issue_ids(const AttnArgs &a, const int32_t *__re
   const int32_t *row = table + (c.row << a.id_shift);
   const int last = c.L - 1 > 0 ? c.L - 1 : 0;
   if (LAYOUT == PAGED16) {
-    if (lane < 2) {
-      int p = c.lt * TILE + 16 * lane;
+    if (lane < G::NH) {
+      int p = c.lt * G::T + 16 * lane;
       p = p < last ? p : last;
       const uint32_t col = min((uint32_t)p >> a.page_shift, a.col_last);
       __builtin_amdgcn_global_load_lds(row + col, (lds_ptr_t)(stage + G::KBYTES + G::VBYTES), 4, 0, 0);
     }
-  } else if (lane < 32) {
-    int p = c.lt * TILE + lane;
+  } else if (lane < G::T) {
+    int p = c.lt * G::T + lane;
     p = p < last ? p : last;
     int64_t col = a.page_size == 1 ? p : p / a.page_size;
     col = col < a.table_width ? col : a.table_width - 1;
@@ -468,26 +471,24 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
                                          int lane, const uint32_t (&loff)[(Geo<D, F8>::NI + W - 1) / W]) {
   using G = Geo<D, F8>;
   constexpr int KPW = (G::NI + W - 1) / W;
-  const int pos0 = ld.c.lt * TILE;
+  const int pos0 = ld.c.lt * G::T;
   const int32_t *ids = reinterpret_cast<const int32_t *>(stage + G::KBYTES + G::VBYTES);
-  uint32_t p0 = 0, p1 = 0;  // PAGED16: pages of the two halves (negative ids wrap high)
-  if (LAYOUT == PAGED16) {
-    p0 = min((uint32_t)__builtin_amdgcn_readfirstlane(ids[0]), a.page_last);
-    p1 = min((uint32_t)__builtin_amdgcn_readfirstlane(ids[1]), a.page_last);
-  }
-  if (LAYOUT != PAGED && pos0 + TILE <= ld.lim) {
-    const char *kh[2], *vh[2];  // first rows of the two halves
-    if (LAYOUT == CONTIG) {
-      kh[0] = ld.kb + (uint64_t)(uint32_t)pos0 * a.k_tok_b;
-      vh[0] = ld.vb + (uint64_t)(uint32_t)pos0 * a.v_tok_b;
-      kh[1] = kh[0] + 16 * a.k_tok_b;
-      vh[1] = vh[0] + 16 * a.v_tok_b;
-    } else {
-      const uint32_t in0 = (uint32_t)pos0 & a.page_mask, in1 = (uint32_t)(pos0 + 16) & a.page_mask;
-      kh[0] = ld.kb + (uint64_t)p0 * a.k_page_b + in0 * a.k_tok_b;
-      vh[0] = ld.vb + (uint64_t)p0 * a.v_page_b + in0 * a.v_tok_b;
-      kh[1] = ld.kb + (uint64_t)p1 * a.k_page_b + in1 * a.k_tok_b;
-      vh[1] = ld.vb + (uint64_t)p1 * a.v_page_b + in1 * a.v_tok_b;
+  uint32_t pg[G::NH];  // PAGED16: pages of the 16-position blocks (negative ids wrap high)
+#pragma unroll
+  for (int q = 0; q < G::NH; ++q)
+    pg[q] = LAYOUT == PAGED16 ? min((uint32_t)__builtin_amdgcn_readfirstlane(ids[q]), a.page_last) : 0u;
+  if (LAYOUT != PAGED && pos0 + G::T <= ld.lim) {
+    const char *kh[G::NH], *vh[G::NH];  // first rows of the 16-position blocks
+#pragma unroll
+    for (int q = 0; q < G::NH; ++q) {
+      if (LAYOUT == CONTIG) {
+        kh[q] = ld.kb + (uint64_t)(uint32_t)(pos0 + 16 * q) * a.k_tok_b;
+        vh[q] = ld.vb + (uint64_t)(uint32_t)(pos0 + 16 * q) * a.v_tok_b;
+      } else {
+        const uint32_t in = (uint32_t)(pos0 + 16 * q) & a.page_mask;
+        kh[q] = ld.kb + (uint64_t)pg[q] * a.k_page_b + in * a.k_tok_b;
+        vh[q] = ld.vb + (uint64_t)pg[q] * a.v_page_b + in * a.v_tok_b;
+      }
     }
 #pragma unroll
     for (int k = 0; k < KPW; ++k) {
@@ -496,8 +497,11 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
       int row, coff, dst;
       bool isk;
       load_slot<D, F8>(i, lane, row, coff, isk, dst);
-      const int hp = row >> 4;  // uniform except for head_dim 64's V blocks
-      const char *base = isk ? (hp ? kh[1] : kh[0]) : (hp ? vh[1] : vh[0]);
+      const int hp = row >> 4;  // uniform except for head_dim 64's bf16 V blocks
+      const char *base = isk ? kh[0] : vh[0];
+#pragma unroll
+      for (int q = 1; q < G::NH; ++q)
+        if (hp == q) base = isk ? kh[q] : vh[q];
       dma16(base + loff[k], stage + dst);
     }
     return;
@@ -520,7 +524,10 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
       const int pc = p < ld.cap ? p : ld.cap - 1;
       off = (uint64_t)(uint32_t)pc * tok_b;
     } else if (LAYOUT == PAGED16) {
-      const uint32_t page = row >= 16 ? p1 : p0;
+      uint32_t page = pg[0];
+#pragma unroll
+      for (int q = 1; q < G::NH; ++q)
+        if ((row >> 4) == q) page = pg[q];
       off = (uint64_t)page * (isk ? a.k_page_b : a.v_page_b) + ((uint32_t)p & a.page_mask) * tok_b;
     } else {
       const uint32_t page = min((uint32_t)ids[row], a.page_last);
@@ -548,10 +555,11 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
                                              const u32x4_t (&qf)[Geo<D, F8>::KC], float sl, f32x4_t (&acc)[D / 16],
                                              float &m, float &l, int pos0, int L, int lane) {
   using G = Geo<D, F8>;
+  constexpr int NH = G::NH;  // 16-position blocks of the tile
   const int g = lane >> 4;
-  f32x4_t s[2];
+  f32x4_t s[NH];
 #pragma unroll
-  for (int pb = 0; pb < 2; ++pb) {
+  for (int pb = 0; pb < NH; ++pb) {
     f32x4_t c = {0.f, 0.f, 0.f, 0.f};
     if constexpr (F8 && G::KC == 2) {  // head_dim 128: one 128-channel fp8 MFMA
       const u32x4_t k0 = *reinterpret_cast<const u32x4_t *>(stage + (pb * 2) * 1024 + lane * 16);
@@ -574,15 +582,16 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
     }
     s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
   }
-  if (pos0 + TILE > L) {
+  if (pos0 + G::T > L) {
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+    for (int pb = 0; pb < NH; ++pb)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (pos0 + 16 * pb + 4 * g + i >= L) s[pb][i] = -INFINITY;
   }
-  float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                   fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+  float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+  for (int pb = 1; pb < NH; ++pb) mx = fmaxf(mx, fmaxf(fmaxf(s[pb][0], s[pb][1]), fmaxf(s[pb][2], s[pb][3])));
   mx = max_over_groups(mx) * sl;
   // Lazy rescale: the reference max m moves only when a row's tile max exceeds it by
   // more than 8 (log2 units), so P <= 2^8 in between and O^T/l are rescaled rarely. This
@@ -595,22 +604,27 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
 #pragma unroll
     for (int db = 0; db < G::DB; ++db) acc[db] *= alpha;
   }
-  float p[2][4];
+  float p[NH][4];
   float ps = 0.f;
 #pragma unroll
-  for (int pb = 0; pb < 2; ++pb)
+  for (int pb = 0; pb < NH; ++pb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       p[pb][i] = __builtin_amdgcn_exp2f(fmaf(s[pb][i], sl, -m));
       ps += p[pb][i];
     }
   l += ps;
-  const u32x4_t pk = {pack_bf16x2(p[0][0], p[0][1]), pack_bf16x2(p[0][2], p[0][3]),
-                      pack_bf16x2(p[1][0], p[1][1]), pack_bf16x2(p[1][2], p[1][3])};
-  if constexpr (F8)
-    pv_accumulate_f8<D>(stage + G::KBYTES, pk, acc, lane);
-  else
-    pv_accumulate<D>(stage + G::KBYTES, pk, acc, lane);
+  // P.V in 32-position halves (the bf16 stage holds one; an e4m3 stage holds its rows
+  // in order, 32 RB bytes per half).
+#pragma unroll
+  for (int h = 0; h < NH / 2; ++h) {
+    const u32x4_t pk = {pack_bf16x2(p[2 * h][0], p[2 * h][1]), pack_bf16x2(p[2 * h][2], p[2 * h][3]),
+                        pack_bf16x2(p[2 * h + 1][0], p[2 * h + 1][1]), pack_bf16x2(p[2 * h + 1][2], p[2 * h + 1][3])};
+    if constexpr (F8)
+      pv_accumulate_f8<D>(stage + G::KBYTES + h * 32 * G::RB, pk, acc, lane);
+    else
+      pv_accumulate<D>(stage + G::KBYTES, pk, acc, lane);
+  }
 }
 
 // pv_accumulate for e4m3 V in the F8 stage layout: one ds_read_b64_tr_b8 per 16-channel
@@ -1285,7 +1299,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       m = -INFINITY;
       l = 0.f;
     }
-    compute_tile<D, F8>(a, stage(i), qf, sl, acc, m, l, cc.lt * TILE, cc.L, lane);
+    compute_tile<D, F8>(a, stage(i), qf, sl, acc, m, l, cc.lt * G::T, cc.L, lane);
     const bool end = cc.lt == cc.tiles - 1 || i == ntiles - 1;
     if (end) {  // the segment ends: its partial
       const float lt_sum = sum_over_groups(l);
@@ -1403,11 +1417,11 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
              mg.acc);
 }
 
-// plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(L_b, 0) / TILE), L_b = seqlens[b], or
+// plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(L_b, 0) / tile), L_b = seqlens[b], or
 // seqlens[b + 1] - seqlens[b] when seqlens is a CSR indptr (csr != 0).
 __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restrict__ seqlens,
                                                          int32_t batch, int32_t *__restrict__ plan,
-                                                         int32_t csr) {
+                                                         int32_t csr, int32_t tile) {
   __shared__ int32_t buf[1024];
   int32_t carry = 0;
   if (threadIdx.x == 0) plan[0] = 0;
@@ -1415,7 +1429,7 @@ __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restri
     const int i = base + threadIdx.x;
     int32_t L = i < batch ? (csr ? seqlens[i + 1] - seqlens[i] : seqlens[i]) : 0;
     L = L > 0 ? L : 0;
-    buf[threadIdx.x] = (L + TILE - 1) / TILE;
+    buf[threadIdx.x] = (L + tile - 1) / tile;
     __syncthreads();
     for (int off = 1; off < 1024; off <<= 1) {
       const int32_t add = threadIdx.x >= (unsigned)off ? buf[threadIdx.x - off] : 0;
@@ -1518,7 +1532,8 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->rp = row_plan(hq / hkv, q_len);
   AttnKernel k = select_kernel(layout, d, sz->rp.nrb, f8);
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
-  const int64_t tiles_bound = ups * batch * (((int64_t)max_k + TILE - 1) / TILE);
+  const int tile = f8 ? TILE_F8 : TILE;
+  const int64_t tiles_bound = ups * batch * (((int64_t)max_k + tile - 1) / tile);
   const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
   const int r = replicas(sz->rp.nrb);
   int64_t nw = (int64_t)info.cus * occupancy(k, 64 * (sz->rp.nrb + 1) * r);
@@ -1604,7 +1619,9 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     a.col_last = (uint32_t)(a.table_width - 1 < 0x7fffffffll ? a.table_width - 1 : 0x7fffffffll);
     a.page_last = (uint32_t)(a.num_pages - 1 < 0xffffffffll ? a.num_pages - 1 : 0xffffffffll);
   }
-  const bool need_plan = a.seqlens != nullptr && c.plan == nullptr;
+  // e4m3 K/V run on tiles of TILE_F8 positions: they always plan for themselves (a
+  // caller's plan counts TILE-position tiles).
+  const bool need_plan = a.seqlens != nullptr && (c.plan == nullptr || a.f8);
   Sizing sz;
   int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, a.f8 != 0);
   if (rc != FM_OK) return rc;
@@ -1642,7 +1659,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   if (a.seqlens != nullptr) {
     if (need_plan) {
       int32_t *plan = (int32_t *)(ws + sz.plan_off);
-      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, plan, a.csr);
+      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, plan, a.csr, a.f8 ? TILE_F8 : TILE);
       FM_CHECK_HIP(hipGetLastError());
       a.plan = plan;
     } else {
@@ -1697,7 +1714,7 @@ extern "C" size_t fm_attn_plan_bytes(int32_t batch) {
 extern "C" int fm_attn_plan(const int32_t *seqlens, int32_t batch, int32_t *plan, void *stream) {
   FM_REQUIRE(batch >= 0, "bad batch");
   FM_REQUIRE(plan != nullptr && (batch == 0 || seqlens != nullptr), "NULL pointer");
-  attn_plan_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(seqlens, batch, plan, 0);
+  attn_plan_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(seqlens, batch, plan, 0, TILE);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
