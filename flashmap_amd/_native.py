@@ -48,6 +48,11 @@ SIGNATURES: dict[str, tuple] = {
         [*_Q, P, I64, I64, I64, I64, I64, I32, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,
          *_PROLOGUE, *_SPLIT],
     ),
+    "fm_block_attn_paged_runs": (
+        c_int,
+        [*_Q, P, P, P, I32, I32, I64, I64, I64, I64, I64, I32, P, I64, I64, P, I32, I32, I32, I32, I32, I32,
+         F32, *_PROLOGUE, *_SPLIT],
+    ),
     "fm_block_attn_token_paged": (
         c_int,
         [*_Q, P, P, I64, I64, I64, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,

@@ -54,6 +54,7 @@ constexpr int TILE_F8 = 64; // e4m3 K/V: the same bytes per tile as bf16
 constexpr int NRB_MAX = 8;  // wavefronts (16-row blocks) per unit
 constexpr int STAGES = 3;     // LDS ring depth (tiles), bf16 K/V
 constexpr int STAGES_F8 = 3;  // e4m3 K/V (tiles of TILE_F8 positions)
+constexpr int MAX_RUNS = 8;   // paged: runs of KV heads over several caches
 
 // Replicas per workgroup: R independent groups of W consumer wavefronts and one producer
 // wavefront, each streaming its own share through its own LDS ring, that meet at one
@@ -90,6 +91,13 @@ struct AttnArgs {
   // place of seqlens); ids are int32, or the low halves of int64 ids with id_shift 1.
   int32_t csr, id_shift;
   int64_t k_s2, v_s2;           // position strides (elements)
+  // Paged layouts: the KV heads in runs over several caches of one geometry (vLLM's
+  // virtual context-cache layout): heads h >= run_head[r] (r < nruns) read K/V from
+  // run_k[r] / run_v[r] + h * head stride, the other heads from u.k / u.v (run 0). The
+  // bases are offset by the run's first cache slot minus its first head.
+  int32_t nruns;
+  int32_t run_head[MAX_RUNS];
+  const char *run_k[MAX_RUNS], *run_v[MAX_RUNS];
   int64_t table_width, num_pages;
   const int32_t *table;
   const int32_t *plan;     // tile prefix over sequences (NULL with seqlens == NULL)
@@ -429,8 +437,12 @@ __device__ __forceinline__ void loader_unit(const AttnArgs &a, Loader &ld) {
     ld.vb = ua.v + ((int64_t)ld.c.b * ua.v_s0 + h * ua.v_s1) * ES;
   } else {
     ld.lim = ld.c.L;
-    ld.kb = ua.k + h * ua.k_s1 * ES;
-    ld.vb = ua.v + h * ua.v_s1 * ES;
+    const char *kb = ua.k, *vb = ua.v;
+#pragma unroll
+    for (int r = 1; r < MAX_RUNS; ++r)
+      if (r < a.nruns && h >= a.run_head[r]) kb = a.run_k[r], vb = a.run_v[r];
+    ld.kb = kb + h * ua.k_s1 * ES;
+    ld.vb = vb + h * ua.v_s1 * ES;
   }
 }
 
@@ -1836,6 +1848,57 @@ extern "C" int fm_block_attn_paged(
   const int rc = setup_paged(a, layout, kv_cache, num_blocks, stride_block, stride_head, stride_token, v_offset,
                              page_size, block_table, block_table_stride, block_table_width, seqused_k, 2);
   return rc != FM_OK ? rc : run_attention(c, layout, a);
+}
+
+extern "C" int fm_block_attn_paged_runs(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head, void *out,
+    int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *const *run_caches, const int32_t *run_first_slot,
+    const int32_t *run_count, int32_t num_runs, int32_t heads_per_cache, int64_t num_blocks,
+    int64_t stride_block, int64_t stride_head, int64_t stride_token, int64_t v_offset, int32_t page_size,
+    const int32_t *block_table, int64_t block_table_stride, int64_t block_table_width,
+    const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+    const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  FM_REQUIRE(run_caches && run_first_slot && run_count, "NULL run arrays");
+  FM_REQUIRE(num_runs >= 1 && num_runs <= MAX_RUNS, "num_runs %d outside [1, %d]", num_runs, MAX_RUNS);
+  FM_REQUIRE(heads_per_cache > 0, "heads_per_cache must be positive");
+  int heads = 0;
+  for (int r = 0; r < num_runs; ++r) {
+    FM_REQUIRE(run_caches[r] != nullptr && al16(run_caches[r]), "run %d: NULL or misaligned cache", r);
+    FM_REQUIRE(run_count[r] > 0 && run_first_slot[r] >= 0 && run_first_slot[r] + run_count[r] <= heads_per_cache,
+               "run %d: slots [%d, %d) outside a cache of %d heads", r, run_first_slot[r],
+               run_first_slot[r] + run_count[r], heads_per_cache);
+    heads += run_count[r];
+  }
+  FM_REQUIRE(heads == num_kv_heads, "the runs hold %d heads, expected num_kv_heads %d", heads, num_kv_heads);
+  CommonIn c{q, q_stride_batch, q_stride_token, q_stride_head, out, out_stride_batch,
+             out_stride_token, out_stride_head, cu_seqlens_q, batch, max_seqlen_q, max_seqlen_k,
+             num_q_heads, num_kv_heads, head_dim, softmax_scale, q_norm_weight, rope_cos,
+             rope_sin, rope_row_stride, rope_pair_stride, rope_rows, q_positions, eps, plan,
+             workspace, workspace_bytes, (hipStream_t)stream};
+  AttnArgs a{};
+  int layout = 0;
+  const int rc = setup_paged(a, layout, run_caches[0], num_blocks, stride_block, stride_head, stride_token,
+                             v_offset, page_size, block_table, block_table_stride, block_table_width, seqused_k, 2);
+  if (rc != FM_OK) return rc;
+  // Run r serves heads [first, first + count) from slots [slot, slot + count): its base is
+  // the cache moved by (slot - first) heads, so that head h sits at base + h * stride_head.
+  a.nruns = num_runs;
+  int first = 0;
+  for (int r = 0; r < num_runs; ++r) {
+    const uintptr_t base = (uintptr_t)run_caches[r] + (uintptr_t)(((int64_t)run_first_slot[r] - first) * stride_head * 2);
+    a.run_head[r] = first;
+    a.run_k[r] = (const char *)base;
+    a.run_v[r] = (const char *)(base + (uintptr_t)(2 * v_offset));
+    first += run_count[r];
+  }
+  a.u.k = a.run_k[0];
+  a.u.v = a.run_v[0];
+  return run_attention(c, layout, a);
 }
 
 extern "C" int fm_block_attn_token_paged(

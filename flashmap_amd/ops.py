@@ -9,6 +9,7 @@ call raises.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -23,6 +24,7 @@ __all__ = [
     "block_attention_contig",
     "block_attention_paged",
     "block_attention_paged_fp8",
+    "block_attention_paged_runs",
     "block_attention_token_paged",
     "block_attention_token_paged_fp8",
     "block_self_attention",
@@ -235,6 +237,7 @@ class Prologue:
 
 
 _NO_PROLOGUE = [None, None, None, 0, 0, 0, None, 0.0]
+MAX_RUNS = 8  # runs of KV heads per fm_block_attn_paged_runs call
 
 
 def _q_out(query: torch.Tensor, out: torch.Tensor | None, varlen: bool):
@@ -325,6 +328,78 @@ def block_attention_paged(
         "fm_block_attn_paged",
         query.data_ptr(), *qs, out.data_ptr(), *os_, _ptr(cu),
         kv_cache.data_ptr(), num_blocks, kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), d, page,
+        bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
+        hq, hkv, d, float(softmax_scale),
+        *(prologue.args() if prologue else _NO_PROLOGUE),
+        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
+    )
+    return out
+
+
+def block_attention_paged_runs(
+    query: torch.Tensor,
+    caches: list[torch.Tensor] | tuple[torch.Tensor, ...],
+    runs: list[tuple[int, int, int, int]],
+    cu_seqlens_q: torch.Tensor | None,
+    seqused_k: torch.Tensor,
+    block_table: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`block_attention_paged` for a layer whose KV heads lie in runs over several
+    vLLM caches of one geometry (the virtual context-cache layout,
+    flashmap/vllm/context_cache.py:33-73): ``runs`` lists ``(cache, first slot, count,
+    first head)`` in head order (a layer's ``ContextCachePlan.segments``), KV head
+    ``first head + i`` of the run at slot ``first slot + i`` of ``caches[cache]``. One
+    launch for all runs, where attend_by_segments makes one call per run and
+    concatenates (flashmap/vllm/context_cache.py:120-139)."""
+    if not runs:
+        raise ValueError("runs must list at least one (cache, first slot, count, first head)")
+    if len(runs) > MAX_RUNS:
+        raise ValueError(f"at most {MAX_RUNS} runs per call, got {len(runs)}")
+    c0 = caches[runs[0][0]]
+    tokens, hq, d = query.shape
+    num_blocks, hpc, page, two_d = c0.shape
+    head = 0
+    for cache_id, first_slot, count, first_head in runs:
+        c = caches[cache_id]
+        if c.dtype != torch.bfloat16:
+            raise TypeError(f"kv caches must be bfloat16, got {c.dtype}")
+        if c.device != c0.device or c.shape != c0.shape or c.stride() != c0.stride():
+            raise ValueError("the runs' caches must share one device, shape and strides")
+        if first_head != head or count <= 0 or first_slot < 0 or first_slot + count > hpc:
+            raise ValueError(f"run {(cache_id, first_slot, count, first_head)} does not continue the heads at {head} "
+                             f"within a cache of {hpc} heads")
+        head += count
+    hkv = head
+    if two_d != 2 * d:
+        raise ValueError(f"kv caches' rows hold {two_d} values, expected 2 * {d}")
+    if c0.stride(-1) != 1:
+        raise ValueError("kv caches must have unit channel stride")
+    _check_cuda(query, c0, cu_seqlens_q, seqused_k, block_table)
+    batch = seqused_k.shape[0]
+    query, out, qs, os_ = _q_out(query, out, varlen=True)
+    if batch == 0 or tokens == 0:
+        return out
+    cu = None if cu_seqlens_q is None else _i32(cu_seqlens_q)
+    if cu is None:
+        qs[0], os_[0] = max_seqlen_q * qs[1], max_seqlen_q * os_[1]
+    bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(-1) == 1) else _i32(block_table)
+    sk = _i32(seqused_k)
+    n = len(runs)
+    ptrs = (ctypes.c_void_p * n)(*[caches[r[0]].data_ptr() for r in runs])
+    slots = (ctypes.c_int32 * n)(*[r[1] for r in runs])
+    counts = (ctypes.c_int32 * n)(*[r[2] for r in runs])
+    ws = workspace_for(batch, max_seqlen_q, hq, hkv, d, max_seqlen_k, query.device)
+    call(
+        "fm_block_attn_paged_runs",
+        query.data_ptr(), *qs, out.data_ptr(), *os_, _ptr(cu),
+        ctypes.addressof(ptrs), ctypes.addressof(slots), ctypes.addressof(counts), n, hpc,
+        num_blocks, c0.stride(0), c0.stride(1), c0.stride(2), d, page,
         bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
         hq, hkv, d, float(softmax_scale),
         *(prologue.args() if prologue else _NO_PROLOGUE),

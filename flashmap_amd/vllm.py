@@ -6,16 +6,17 @@ and engine graphs capture them:
 
 - ``flashmap_vllm::rms_norm_rope``          (flashmap/vllm/kernels.py:101-124)
 - ``flashmap_vllm::block_self_attention``   (flashmap/vllm/kernels.py:194-232)
-- ``flashmap_vllm::paged_cross_attention``  (flashmap/vllm/model.py:93-139)
+- ``flashmap_vllm::paged_cross_attention``  (flashmap/vllm/model.py:93-139), bf16
+  caches and e4m3 caches with ``descales``
 
-plus the plain functions :func:`write_context_kv` (flashmap/vllm/kernels.py:311-364)
-and :func:`cross_attention_schedule`, the per-step plan that takes the place of
-FlashAttention's ``get_scheduler_metadata`` (flashmap/vllm/model.py:967-989): pass its
-result as ``scheduler_metadata``. Registration is explicit (not on import) so the
+plus ``flashmap_vllm::paged_cross_attention_runs``, one DiT layer's cross-attention
+over the virtual context-cache layout in one launch (what attend_by_segments does with
+one call per run, flashmap/vllm/context_cache.py:120-139), and the plain functions
+:func:`write_context_kv` (flashmap/vllm/kernels.py:311-364; bf16, or e4m3 with
+``scales``) and :func:`cross_attention_schedule`, the per-step plan that takes the place
+of FlashAttention's ``get_scheduler_metadata`` (flashmap/vllm/model.py:967-989): pass
+its result as ``scheduler_metadata``. Registration is explicit (not on import) so the
 package can sit beside the reference plugin; it is idempotent.
-
-Not implemented (raising ``NotImplementedError``): fp8 (e4m3) caches, i.e. non-None
-``descales`` / ``scales``.
 """
 
 from __future__ import annotations
@@ -97,6 +98,32 @@ def paged_cross_attention(
     )
 
 
+def paged_cross_attention_runs(
+    query: torch.Tensor,
+    kv_caches: list[torch.Tensor],
+    runs: list[int],
+    cu_seqlens_q: torch.Tensor,
+    seqused_k: torch.Tensor,
+    block_table: torch.Tensor,
+    scheduler_metadata: torch.Tensor | None,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+) -> torch.Tensor:
+    """:func:`paged_cross_attention` of one DiT layer whose KV heads lie in runs over
+    several bf16 caches (``ContextCachePlan.segments[layer]`` flattened, four ints per
+    run: cache, first slot, count, first head), in one launch; the output is what
+    attend_by_segments concatenates from one call per run
+    (flashmap/vllm/context_cache.py:120-139)."""
+    if len(runs) % 4:
+        raise ValueError("runs must hold four ints per run (cache, first slot, count, first head)")
+    segments = [tuple(runs[i:i + 4]) for i in range(0, len(runs), 4)]
+    return ops.block_attention_paged_runs(
+        query, kv_caches, segments, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k,
+        softmax_scale, plan=_plan(scheduler_metadata, seqused_k.shape[0]),
+    )
+
+
 def write_context_kv(
     kv: torch.Tensor,
     positions: torch.Tensor,
@@ -150,10 +177,13 @@ def register(namespace: str = NAMESPACE) -> dict[str, object]:
         return torch.empty(query.shape, dtype=torch.bfloat16, device=query.device)
 
     cross.register_fake(_cross_fake)
+
+    runs = lib.custom_op(f"{namespace}::paged_cross_attention_runs", mutates_args=())(paged_cross_attention_runs)
+    runs.register_fake(lambda query, *args: torch.empty_like(query))
     _OPS[namespace] = {"rms_norm_rope": norm, "block_self_attention": self_attn,
-                       "paged_cross_attention": cross}
+                       "paged_cross_attention": cross, "paged_cross_attention_runs": runs}
     return _OPS[namespace]
 
 
-__all__ = ["block_self_attention", "cross_attention_schedule", "paged_cross_attention", "register",
-           "rms_norm_rope", "write_context_kv"]
+__all__ = ["block_self_attention", "cross_attention_schedule", "paged_cross_attention",
+           "paged_cross_attention_runs", "register", "rms_norm_rope", "write_context_kv"]

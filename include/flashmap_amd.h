@@ -145,6 +145,28 @@ int fm_block_attn_paged(
     const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
     size_t workspace_bytes, void *stream);
 
+/* f4: one drafter layer's paged attention over vLLM's virtual context-cache layout
+ * (flashmap/vllm/context_cache.py:33-73), where the layer's KV heads lie in runs across
+ * several caches of one geometry and one block table: run r holds the next run_count[r]
+ * KV heads (in order, from head 0) at head slots run_first_slot[r] .. of the cache at
+ * run_caches[r] (a host array of device pointers; heads_per_cache heads per cache). One
+ * launch replaces attend_by_segments' per-run flashmap_vllm::paged_cross_attention calls
+ * and the concatenation of their outputs (flashmap/vllm/context_cache.py:120-139, called
+ * at flashmap/vllm/model.py:874-893). The other arguments are fm_block_attn_paged's. */
+int fm_block_attn_paged_runs(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *const *run_caches, const int32_t *run_first_slot,
+    const int32_t *run_count, int32_t num_runs, int32_t heads_per_cache, int64_t num_blocks,
+    int64_t stride_block, int64_t stride_head, int64_t stride_token, int64_t v_offset,
+    int32_t page_size, const int32_t *block_table, int64_t block_table_stride,
+    int64_t block_table_width, const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q,
+    int32_t max_seqlen_k, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
+    size_t workspace_bytes, void *stream);
+
 /* a7: token-paged KV, SGLang's pool ((pool_size, kv_heads, head_dim) key and value
  * buffers): position p of sequence b is pool row page_table[b * page_table_stride + p]
  * (flashmap/sglang/model.py:127-151, 785-786, 861-864). Pool rows are clamped into

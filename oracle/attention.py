@@ -336,6 +336,47 @@ def write_context_kv_vllm(kv, positions, slots, k_norm, cos_sin, caches, block_s
                 caches[c][page, s, tok, d:] = kv[t, l, 1, h]
 
 
+# ------------------------------------------------------ virtual context-cache layout
+
+
+def context_segments(num_layers: int, heads: int, heads_per_cache: int):
+    """Per DiT layer, its heads as runs ``(cache, first slot, count, first head)``, built
+    head by head as ``ContextCachePlan.segments`` does (flashmap/vllm/context_cache.py:56-68):
+    global head ``l * heads + h`` sits at ``divmod(., heads_per_cache)`` (:60-73), and a
+    head in the same cache as the previous one extends its run. Pinned by: the runs
+    cover the heads in order, give each head the closed-form (cache, slot), and
+    neighbouring runs lie in different caches, which fixes them (test_context_cache)."""
+    out = []
+    for layer in range(num_layers):
+        runs: list[tuple[int, int, int, int]] = []
+        for head in range(heads):
+            cache, slot = divmod(layer * heads + head, heads_per_cache)
+            if runs and runs[-1][0] == cache:
+                c, first_slot, count, first_head = runs[-1]
+                runs[-1] = (c, first_slot, count + 1, first_head)
+            else:
+                runs.append((cache, slot, 1, head))
+        out.append(runs)
+    return out
+
+
+def block_attention_paged_segments(query, caches, segments, cu_seqlens_q, seqused_k, block_table, scale=None):
+    """One layer's cross-attention over the virtual layout: block_attention_paged_vllm
+    per run, on the run's query heads and cache heads, concatenated along the heads
+    (flashmap/vllm/context_cache.py:120-139 with the op of flashmap/vllm/model.py:876-890;
+    ``G`` query heads per KV head). Pinned by: equal to block_attention_paged_vllm on a
+    per-layer cache that holds the same heads, gathered by the closed-form (cache, slot)
+    map (test_context_cache)."""
+    kv_heads = sum(run[2] for run in segments)
+    group = query.shape[1] // kv_heads
+    parts = []
+    for cache_id, first_slot, count, first_head in segments:
+        q = query[:, group * first_head:group * (first_head + count)]
+        c = caches[cache_id][:, first_slot:first_slot + count]
+        parts.append(block_attention_paged_vllm(q, c, cu_seqlens_q, seqused_k, block_table, scale))
+    return torch.cat(parts, dim=1)
+
+
 # ------------------------------------------------------------------- fp8 (e4m3) KV
 
 

@@ -26,7 +26,8 @@ def ns():
 def test_register_is_idempotent():
     a = fv.register("fm_cpu_test_vllm_idem")
     assert fv.register("fm_cpu_test_vllm_idem") is a
-    assert set(a) == {"rms_norm_rope", "block_self_attention", "paged_cross_attention"}
+    assert set(a) == {"rms_norm_rope", "block_self_attention", "paged_cross_attention",
+                      "paged_cross_attention_runs"}
 
 
 def test_vllm_fake_shapes(ns):
@@ -41,6 +42,11 @@ def test_vllm_fake_shapes(ns):
     qkv = _e(3, 16, 3, 4, 128, dtype=torch.bfloat16)
     got = v.block_self_attention(qkv, _e(128), _e(128), _e(100, 64, 2), _e(48, dtype=torch.long), 1e-6)
     assert got.shape == (48, 512) and got.dtype == torch.bfloat16
+    caches = [_e(100, 8, 16, 256, dtype=torch.bfloat16) for _ in range(3)]
+    runs = v.paged_cross_attention_runs(q[:, :20], caches, [0, 0, 8, 0, 1, 0, 8, 8, 2, 0, 4, 16],
+                                        _e(65, dtype=torch.int32), _e(64, dtype=torch.int32),
+                                        _e(64, 10, dtype=torch.int32), None, 16, 8192, 0.088)
+    assert runs.shape == (64 * 16, 20, 128) and runs.dtype == torch.bfloat16
 
 
 def test_sglang_fake_shapes(ns):
