@@ -168,6 +168,130 @@ VERIFY_WORKLOADS = {
 }
 
 
+# The drafter workload over vLLM's virtual context-cache layout: name -> (the bf16
+# workload whose draw it shares, heads per cache, DiT layer timed). The context writer
+# packs (layer + 1) DiT layers' heads into caches of that many heads (each layer's K/V
+# the shared draw); the timed layer's KV heads then lie in several runs and one launch
+# attends to them all.
+VIRTUAL_WORKLOADS = {
+    "c3-qwen3-8b-virtual-hpc3": ("c3-qwen3-8b-paged-b64", 3, 1),
+}
+
+# Tree drafting on SGLang's token pool: name -> (requests, hq, hkv, head_dim, candidates,
+# ctx lo, ctx hi). A request's candidate blocks sit side by side in the query axis
+# (n_cand * 16 rows) over its one context (the reference's MHA drafter shape, the
+# candidate counts its default budget of 32 gives at batch 1 and 4).
+TREE_WORKLOADS = {
+    "tree-r8b-b1-n32": (1, 16, 16, 128, 32, 8192, 8192),
+    "tree-r8b-b4-n8": (4, 16, 16, 128, 8, 1024, 8192),
+}
+
+
+def _time_call(call, args) -> tuple[float, float]:
+    """(ms per call, ms per main-kernel launch from the library's HIP events)."""
+    import ctypes
+
+    from flashmap_amd import _native
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    lib = _native.lib()
+    lib.fm_profile_enable(1)
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    tot, cnt = ctypes.c_double(), ctypes.c_int64()
+    _native.call("fm_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
+    lib.fm_profile_enable(0)
+    return ms, tot.value / max(cnt.value, 1)
+
+
+def run_tree(args, dev) -> dict:
+    """One call = flashmap_sglang::paged_cross_attention of every request's candidates
+    side by side: query packing, the split-KV stream and the combine."""
+    from flashmap_amd import ops
+
+    requests, hq, hkv, d, n_cand, lo, hi = TREE_WORKLOADS[args.workload]
+    k_rows = 16
+    q_len = n_cand * k_rows
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(lo, hi + 1, (requests,), generator=g)
+    ctx = int(lens.sum())
+    slots = torch.randperm(ctx, generator=g).to(torch.int32)
+    pt = torch.zeros(requests, hi, dtype=torch.int32)
+    o = 0
+    for b in range(requests):
+        pt[b, :int(lens[b])] = slots[o:o + int(lens[b])]
+        o += int(lens[b])
+    q = torch.randn(requests, q_len, hq, d, generator=g).bfloat16().to(dev)
+    kb = torch.randn(ctx, hkv, d, generator=g).bfloat16().to(dev)
+    vb = torch.randn(ctx, hkv, d, generator=g).bfloat16().to(dev)
+    lens_d, pt_d = lens.to(dev, torch.int32), pt.to(dev)
+    plan = ops.attention_plan(lens_d)
+    out = torch.empty_like(q)
+
+    def call():
+        ops.block_attention_token_paged(q, kb, vb, lens_d, pt_d, plan=plan, out=out)
+
+    ms, kernel_ms = _time_call(call, args)
+    kv = ctx * hkv * d * 2 * 2
+    total = kv + 4 * ctx + 4 * requests + 2 * requests * q_len * hq * d * 2
+    flops = 4 * q_len * hq * d * ctx
+    gbs = total / (kernel_ms * 1e-3) / 1e9
+    tflops = flops / (kernel_ms * 1e-3) / 1e12
+    hbm_frac, mfma_frac = gbs / HBM_PEAK_GBS, tflops / MFMA_BF16_PEAK_TFLOPS
+    mfma_bound = flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) > total / (HBM_PEAK_GBS * 1e9)
+    result = {
+        "metric": "tree-drafting cross-attn µs/call, n_cand x 16 rows per request, 1 GPU",
+        "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: seeded CPU draw (lengths, pool slots, q, K/V)",
+        "config": {"workload": args.workload, "requests": requests, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+                   "candidates": n_cand, "q_rows_per_request": q_len, "ctx_lo": lo, "ctx_hi": hi, "ctx_sum": ctx,
+                   "layout": "sglang token pool (pool, kv_heads, head_dim), page table"},
+        "roofline": ({"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(mfma_frac, 4)} if mfma_bound else
+                     {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(hbm_frac, 4)}),
+        "hbm_frac": round(hbm_frac, 4), "mfma_frac": round(mfma_frac, 4),
+    }
+    result["roofline"].update({"kernel": "attn_fwd_kernel", "traffic": None, "bytes_per_launch": total,
+                               "flops_per_launch": flops, "kernel_us": round(kernel_ms * 1e3, 2)})
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = tree_cpu_baseline(q, kb, vb, lens, pt, args.cpu_budget)
+    return result
+
+
+def tree_cpu_baseline(q, kb, vb, lens, pt, budget_s) -> dict:
+    """The token-paged oracle on the host cores, request by request until the budget is
+    spent, scaled to the whole call by context positions."""
+    from oracle import attention as ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc, vc, qc = kb.cpu(), vb.cpu(), q.cpu()
+    done_l = done = 0
+    t0 = time.perf_counter()
+    for b in range(len(lens)):
+        ref.block_attention_token_paged(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
+        done_l += int(lens[b])
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    return {"value": round(elapsed * int(lens.sum()) / done_l * 1e6, 1), "unit": "us/call", "cores": cores,
+            "kind": "port", "sample": f"first {done} of {len(lens)} requests ({done_l} context positions): "
+                                      "fp32 oracle token-paged attention, scaled by positions"}
+
+
 def run_verify(args, dev) -> dict:
     """One call = fm_verify_attention over the batch: plan, query packing, the split-KV
     stream of every request's context, and the combine that attends the verify tokens
@@ -286,7 +410,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64",
-                    choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS))
+                    choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS)
+                    + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", type=int, default=0,
@@ -309,12 +434,16 @@ def main() -> int:
     if args.workload in VERIFY_WORKLOADS:
         print(json.dumps(run_verify(args, dev)))
         return 0
+    if args.workload in TREE_WORKLOADS:
+        print(json.dumps(run_tree(args, dev)))
+        return 0
 
     from flashmap_amd import _native, ops
     from oracle import attention as ref
 
     fp8 = args.workload in FP8_WORKLOADS
-    inp = build_inputs(FP8_WORKLOADS.get(args.workload, args.workload))
+    virtual = VIRTUAL_WORKLOADS.get(args.workload)
+    inp = build_inputs(FP8_WORKLOADS.get(args.workload) or (virtual[0] if virtual else args.workload))
     batch, hq, hkv, d, k_rows, page = (inp[k] for k in ("batch", "hq", "hkv", "d", "k_rows", "page"))
     table = ref.rope_table(inp["hi"] + k_rows + 1, d, 1e6).to(dev)
     rope = ops.rope_from_table(table)
@@ -326,7 +455,22 @@ def main() -> int:
     writer_args = (inp["kv_pre"].to(dev), inp["positions"].to(dev), inp["slots"].to(dev),
                    w[None].expand(1, d).contiguous(), rope, ptrs,
                    (cache.stride(0), cache.stride(1), cache.stride(2), d), page, 1e-6)
-    if fp8:
+    runs = None
+    if virtual:  # (layer + 1) DiT layers packed into caches of hpc heads
+        from flashmap_amd import context_cache as cc
+
+        _, hpc, layer = virtual
+        vplan = cc.ContextCachePlan(layer + 1, hkv, -(-(layer + 1) * hkv // hpc), hpc, True, "")
+        del cache
+        caches = [torch.zeros(inp["total"], hpc, page, 2 * d, dtype=torch.bfloat16, device=dev)
+                  for _ in range(vplan.num_caches)]
+        c0 = caches[0]
+        ops.write_context_kv(inp["kv_pre"].to(dev).repeat(1, layer + 1, 1, 1, 1), inp["positions"].to(dev),
+                             inp["slots"].to(dev), w[None].expand(layer + 1, d).contiguous(), rope,
+                             torch.tensor([c.data_ptr() for c in caches], dtype=torch.int64, device=dev),
+                             (c0.stride(0), c0.stride(1), c0.stride(2), d), page, 1e-6, heads_per_cache=hpc)
+        runs = vplan.segments[layer]
+    elif fp8:
         ops.write_context_kv_fp8(*writer_args, torch.ones(1, 2, device=dev))
     else:
         ops.write_context_kv(*writer_args)
@@ -339,7 +483,10 @@ def main() -> int:
     out = torch.empty_like(q_pre)
 
     def call():
-        if fp8:
+        if runs is not None:
+            ops.block_attention_paged_runs(q_pre, caches, runs, cu, lens, bt, k_rows, max_k, d ** -0.5,
+                                           prologue=pro, plan=plan, out=out)
+        elif fp8:
             ops.block_attention_paged_fp8(q_pre, cache, cu, lens, bt, k_rows, max_k, d ** -0.5,
                                           prologue=pro, plan=plan, out=out)
         else:
@@ -397,7 +544,9 @@ def main() -> int:
             "workload": args.workload,
             "batch": batch, "q_heads": hq, "kv_heads": hkv, "head_dim": d, "block_queries": k_rows,
             "ctx_lo": inp["lo"], "ctx_hi": inp["hi"], "ctx_sum": ab["sum_l"], "page": page,
-            "layout": "vllm paged (blocks, kv_heads, page, 2*head_dim)", "prologue": "fused",
+            "layout": "vllm paged (blocks, kv_heads, page, 2*head_dim)" + (
+                f", virtual context-cache layout: caches of {virtual[1]} heads, runs {runs}" if virtual else ""),
+            "prologue": "fused",
             "kv_dtype": "e4m3" if fp8 else "bf16",
         },
         "hbm_tbs": round(ab["total"] / (ms * 1e-3) / 1e12, 3),
