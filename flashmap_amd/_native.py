@@ -91,6 +91,10 @@ SIGNATURES: dict[str, tuple] = {
     "fm_write_context_kv_pool_fp8": (
         c_int, [P, I64, I32, I32, I32, P, P, *_ROPE, P, P, P, I64, F32, F32, F32, P]
     ),
+    "fm_select_workspace_bytes": (c_size_t, [I64, I64]),
+    "fm_argmax_rows": (c_int, [P, I32, I64, I64, I64, P, P, c_size_t, P]),
+    "fm_sample_rows": (c_int, [P, I32, I64, I64, I64, P, P, P, P, P, c_size_t, P]),
+    "fm_seeded_normal": (c_int, [P, P, I32, P, I32, I64, I64, F32, P, I64, P]),
     "fm_profile_enable": (c_int, [c_int]),
     "fm_profile_read": (c_int, [ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]),
 }

@@ -20,6 +20,7 @@ from ._native import call
 
 __all__ = [
     "Rope",
+    "argmax_rows",
     "attention_plan",
     "block_attention_contig",
     "block_attention_paged",
@@ -32,6 +33,8 @@ __all__ = [
     "rope_from_cat",
     "rope_from_split",
     "rope_from_table",
+    "sample_rows",
+    "seeded_normal",
     "verify_attention",
     "verify_workspace_bytes",
     "workspace_for",
@@ -862,6 +865,82 @@ def write_context_kv_pool_fp8(
         _f32(k_norm_weights).data_ptr(), *rope.args(), _i64(positions).data_ptr(), _i64(locs).data_ptr(),
         _ptr(cl), int(locs_row_width or 0), float(k_scale), float(v_scale), float(eps), _stream(kv),
     )
+
+
+# ------------------------------------------------------------ token selection and noise
+
+_LOGIT_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _logits(logits: torch.Tensor) -> torch.Tensor:
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be (rows, vocab), got {tuple(logits.shape)}")
+    if logits.dtype not in _LOGIT_DTYPES:
+        raise TypeError(f"logits must be bfloat16, float16 or float32, got {logits.dtype}")
+    return logits if logits.stride(-1) == 1 else logits.contiguous()
+
+
+def _select(name: str, logits: torch.Tensor, *extra) -> torch.Tensor:
+    rows, vocab = logits.shape
+    out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    if rows == 0:
+        return out
+    if vocab == 0:
+        raise ValueError("an empty vocabulary has no argmax")
+    ws = torch.empty(max(int(_native.lib().fm_select_workspace_bytes(rows, vocab)), 1), dtype=torch.uint8,
+                     device=logits.device)
+    call(name, logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], rows, vocab, logits.stride(0), *extra,
+         out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(logits))
+    return out
+
+
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """Per row of ``logits (rows, vocab)`` (bf16, fp16 or fp32) the int64 index of the
+    largest value, the first among equals, a NaN counting as the largest: ``argmax(-1)``
+    as flashmap/vllm/fold.py:117-128 (split_argmax) computes it."""
+    _check_cuda(logits)
+    return _select("fm_argmax_rows", _logits(logits))
+
+
+def sample_rows(
+    logits: torch.Tensor, temperatures: torch.Tensor, greedy: torch.Tensor, seed: torch.Tensor
+) -> torch.Tensor:
+    """A token per row of ``logits (rows, V)``: the argmax for rows where ``greedy`` is
+    set, else a sample of softmax(logits / temperature) by Gumbel-max with Triton's
+    Philox noise ``tl.rand(seed, row * V + col)`` (flashmap/sglang/kernels.py:195-247);
+    ``seed`` is an int64 scalar tensor (advance it between calls for fresh noise)."""
+    _check_cuda(logits, temperatures, greedy, seed)
+    logits = _logits(logits)
+    rows = logits.shape[0]
+    if temperatures.numel() != rows or greedy.numel() != rows:
+        raise ValueError(f"temperatures and greedy must hold one entry per row ({rows})")
+    if seed.dtype != torch.int64 or seed.numel() != 1:
+        raise TypeError("seed must be an int64 scalar tensor")
+    g = greedy if (greedy.dtype in (torch.bool, torch.uint8) and greedy.is_contiguous()) else (greedy != 0)
+    g = g.view(torch.uint8) if g.dtype == torch.bool else g
+    return _select("fm_sample_rows", logits, _f32(temperatures).data_ptr(), g.contiguous().data_ptr(),
+                   seed.data_ptr())
+
+
+def seeded_normal(
+    seeds: torch.Tensor, rows: torch.Tensor, positions: torch.Tensor, n_cols: int, scale: float = 1.0
+) -> torch.Tensor:
+    """Standard normals ``(len(rows), n_cols)`` in float32 times ``scale``, row ``i``
+    keyed by ``seeds[rows[i]] * 1000003 + positions[i]`` (seed 0 where ``rows[i] < 0``),
+    column ``j`` at offset ``j``: Triton's ``tl.randn`` stream as
+    flashmap/vllm/kernels.py:367-410 draws it. ``rows[i]`` must index ``seeds``."""
+    _check_cuda(seeds, rows, positions)
+    n = rows.shape[0]
+    out = torch.empty(n, n_cols, dtype=torch.float32, device=rows.device)
+    if n == 0 or n_cols == 0:
+        return out
+    if positions.shape[0] != n:
+        raise ValueError("positions must hold one entry per row")
+    r = rows if (rows.dtype in (torch.int32, torch.int64) and rows.is_contiguous()) else _i64(rows)
+    p = positions if (positions.dtype in (torch.int32, torch.int64) and positions.is_contiguous()) else _i64(positions)
+    call("fm_seeded_normal", _i64(seeds).data_ptr(), r.data_ptr(), int(r.dtype == torch.int64), p.data_ptr(),
+         int(p.dtype == torch.int64), n, n_cols, float(scale), out.data_ptr(), out.stride(0), _stream(rows))
+    return out
 
 
 def default_scale(head_dim: int) -> float:

@@ -144,6 +144,25 @@ def fused_kv_norm_rope_write(
                               num_layers, kv_size, head_dim, eps, commit_lens, locs_row_width)
 
 
+def sample_rows(
+    logits: torch.Tensor,
+    temperatures: torch.Tensor,
+    greedy: torch.Tensor,
+    seed: torch.Tensor,
+    block_v: int = 4096,
+) -> torch.Tensor:
+    """A token per row of contiguous ``logits (rows, V)``: the argmax for ``greedy`` rows,
+    else a sample of ``softmax(logits / temperature)`` (Gumbel-max), with Philox noise
+    seeded by the int64 scalar tensor ``seed`` (flashmap/sglang/kernels.py:222-247); the
+    tokens equal the reference's for the same seed wherever the winning key is not
+    within float rounding of the runner-up. ``block_v`` is accepted for the signature
+    (the tiling does not change the result). Reads the logits once; no noise buffer."""
+    del block_v
+    if not logits.is_contiguous():
+        raise ValueError("logits must be contiguous")
+    return ops.sample_rows(logits, temperatures, greedy, seed)
+
+
 _OPS: dict[str, object] = {}
 
 
@@ -175,4 +194,4 @@ def register(namespace: str = NAMESPACE) -> dict[str, object]:
 
 __all__ = ["block_self_attention", "cross_attention_schedule", "fused_kv_norm_rope_write",
            "kv_norm_rope_write_fp8", "paged_cross_attention", "paged_cross_attention_fp8", "register",
-           "rms_norm_rope", "rope_freqs"]
+           "rms_norm_rope", "rope_freqs", "sample_rows"]

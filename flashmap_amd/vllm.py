@@ -150,6 +150,23 @@ def write_context_kv(
                          cache_strides, block_size, eps, heads_per_cache)
 
 
+def split_argmax(logits: torch.Tensor, chunks: int = 128) -> torch.Tensor:
+    """``logits.argmax(-1)`` of ``(rows, vocab)`` logits, the first index among equals
+    (flashmap/vllm/fold.py:117-128). ``chunks`` is accepted for the signature: the kernel
+    splits the vocabulary into tiles of its own, which does not change the result."""
+    del chunks
+    return ops.argmax_rows(logits)
+
+
+def seeded_normal(
+    seeds: torch.Tensor, rows: torch.Tensor, positions: torch.Tensor, n_cols: int, scale: float = 1.0
+) -> torch.Tensor:
+    """Standard normals ``(len(rows), n_cols)`` in float32, row ``i`` keyed by
+    ``seeds[rows[i]]`` (0 where ``rows[i] < 0``) and ``positions[i]``
+    (flashmap/vllm/kernels.py:394-410), the reference's random stream."""
+    return ops.seeded_normal(seeds, rows, positions, n_cols, scale)
+
+
 _OPS: dict[str, object] = {}
 
 
@@ -186,4 +203,5 @@ def register(namespace: str = NAMESPACE) -> dict[str, object]:
 
 
 __all__ = ["block_self_attention", "cross_attention_schedule", "paged_cross_attention",
-           "paged_cross_attention_runs", "register", "rms_norm_rope", "write_context_kv"]
+           "paged_cross_attention_runs", "register", "rms_norm_rope", "seeded_normal", "split_argmax",
+           "write_context_kv"]

@@ -353,6 +353,37 @@ int fm_write_context_kv_pool_fp8(const void *kv, int64_t tokens, int32_t layers,
                                  float k_scale, float v_scale, float eps, void *stream);
 
 /* ---------------------------------------------------------------------------------
+ * f3: the draft step's token selection and noise. Logits are (rows, vocab) with
+ * row_stride elements between rows, dtype 0 bf16, 1 fp16, 2 fp32; out is int64 (rows,).
+ * The selection calls use a caller workspace of fm_select_workspace_bytes(rows, vocab)
+ * bytes. The random stream is Triton's tl.rand / tl.randn (Philox-4x32-10 keyed by the
+ * seed's words, counter (offset, 0, 0, 0)) word for word.
+ */
+size_t fm_select_workspace_bytes(int64_t rows, int64_t vocab);
+/* split_argmax (flashmap/vllm/fold.py:117-128, called at flashmap/vllm/speculator.py:218):
+ * per row the index of the largest logit, the first among equals (a NaN counts as the
+ * largest). */
+int fm_argmax_rows(const void *logits, int32_t dtype, int64_t rows, int64_t vocab,
+                   int64_t row_stride, int64_t *out, void *workspace, size_t workspace_bytes,
+                   void *stream);
+/* sample_rows (flashmap/sglang/kernels.py:195-247, called at flashmap/sglang/sampler.py:169):
+ * per row the argmax of its logits where greedy[row] != 0, else of
+ * logit / temperatures[row] - log(-log(u)), u = tl.rand(*seed, row * vocab + col) with
+ * int32 offsets (Gumbel-max); the first index among equals. seed: a device int64. */
+int fm_sample_rows(const void *logits, int32_t dtype, int64_t rows, int64_t vocab,
+                   int64_t row_stride, const float *temperatures, const uint8_t *greedy,
+                   const int64_t *seed, int64_t *out, void *workspace, size_t workspace_bytes,
+                   void *stream);
+/* seeded_normal (flashmap/vllm/kernels.py:367-410, called at flashmap/vllm/model.py:965):
+ * out[i, j] = scale * tl.randn(key_i, j), key_i = seeds[rows[i]] * 1000003 + positions[i]
+ * (int64, wrapping; seed 0 where rows[i] < 0). rows / positions are int64 where their
+ * flag is nonzero, else int32; rows[i] must index seeds. */
+int fm_seeded_normal(const int64_t *seeds, const void *rows, int32_t rows_int64,
+                     const void *positions, int32_t positions_int64, int64_t num_rows,
+                     int64_t n_cols, float scale, float *out, int64_t out_row_stride,
+                     void *stream);
+
+/* ---------------------------------------------------------------------------------
  * Measurement hook. No reference counterpart: it lets a benchmark time the main
  * split-KV attention kernel alone with HIP events on the stream it runs on, without
  * changing the work any call does. While enabled, every attention call records an
