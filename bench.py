@@ -187,6 +187,74 @@ TREE_WORKLOADS = {
 }
 
 
+# The draft step's token selection over bf16 logits: name -> (rows, vocabulary, mode).
+# Rows = 64 requests x 16 draft rows; Qwen3's vocabulary. "argmax": split_argmax (vLLM's
+# greedy draft); "sample": sample_rows with every row sampled (SGLang's fused sampler,
+# Gumbel-max on the Philox stream).
+SELECT_WORKLOADS = {
+    "argmax-b64x16-v151936": (1024, 151936, "argmax"),
+    "sample-b64x16-v151936": (1024, 151936, "sample"),
+}
+
+
+def run_select(args, dev) -> dict:
+    """One call = one selection over the logits (tile pass + row pass)."""
+    from flashmap_amd import ops
+
+    rows, vocab, mode = SELECT_WORKLOADS[args.workload]
+    g = torch.Generator(device=dev).manual_seed(0)
+    logits = torch.randn(rows, vocab, generator=g, device=dev, dtype=torch.bfloat16)
+    temps = torch.full((rows,), 0.8, device=dev)
+    greedy = torch.zeros(rows, dtype=torch.bool, device=dev)
+    seed = torch.tensor(1, dtype=torch.int64, device=dev)
+    if mode == "argmax":
+        def call():
+            ops.argmax_rows(logits)
+    else:
+        def call():
+            ops.sample_rows(logits, temps, greedy, seed)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    total = rows * vocab * 2 + rows * 8
+    gbs = total / (ms * 1e-3) / 1e9
+    result = {
+        "metric": f"draft-step token selection µs/call ({mode}), {rows} rows x {vocab} bf16 logits, 1 GPU",
+        "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 logits, fp32 keys", "data": "synthetic: seeded GPU draw of the logits",
+        "config": {"workload": args.workload, "rows": rows, "vocab": vocab, "mode": mode},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": total,
+                     "note": "whole call (tile pass + row pass) from events around the calls"
+                             + ("; the sampled path is ALU-bound: one Philox-4x32-10 and two logs per logit"
+                                if mode == "sample" else "")},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import sampling as S
+
+        cores = len(os.sched_getaffinity(0))
+        n = 16
+        x = logits[:n].float().cpu().numpy()
+        t0 = time.perf_counter()
+        if mode == "argmax":
+            S.split_argmax(x)
+        else:
+            S.sample_rows(x, temps[:n].cpu().numpy(), greedy[:n].cpu().numpy(), 1)
+        el = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(el * rows / n * 1e6, 1), "unit": "us/call", "cores": 1,
+                                  "kind": "port", "sample": f"first {n} of {rows} rows, numpy oracle, "
+                                                            "scaled by rows"}
+    return result
+
+
 def _time_call(call, args) -> tuple[float, float]:
     """(ms per call, ms per main-kernel launch from the library's HIP events)."""
     import ctypes
@@ -411,7 +479,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64",
                     choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS)
-                    + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS))
+                    + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS) + sorted(SELECT_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", type=int, default=0,
@@ -436,6 +504,9 @@ def main() -> int:
         return 0
     if args.workload in TREE_WORKLOADS:
         print(json.dumps(run_tree(args, dev)))
+        return 0
+    if args.workload in SELECT_WORKLOADS:
+        print(json.dumps(run_select(args, dev)))
         return 0
 
     from flashmap_amd import _native, ops
