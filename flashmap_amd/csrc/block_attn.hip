@@ -1431,26 +1431,34 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
 
 // plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(L_b, 0) / tile), L_b = seqlens[b], or
 // seqlens[b + 1] - seqlens[b] when seqlens is a CSR indptr (csr != 0).
+// The plan holds two tile prefixes, for bf16 K/V (TILE positions) at plan[0 .. batch] and
+// for e4m3 K/V (TILE_F8) at plan[batch + 1 .. 2 batch + 1], so one step plan serves calls
+// of either kind.
 __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restrict__ seqlens,
                                                          int32_t batch, int32_t *__restrict__ plan,
-                                                         int32_t csr, int32_t tile) {
-  __shared__ int32_t buf[1024];
-  int32_t carry = 0;
-  if (threadIdx.x == 0) plan[0] = 0;
+                                                         int32_t csr) {
+  __shared__ int32_t buf[2][1024];
+  int32_t carry[2] = {0, 0};
+  int32_t *out[2] = {plan, plan + batch + 1};
+  if (threadIdx.x == 0) out[0][0] = 0, out[1][0] = 0;
   for (int base = 0; base < batch; base += 1024) {
     const int i = base + threadIdx.x;
     int32_t L = i < batch ? (csr ? seqlens[i + 1] - seqlens[i] : seqlens[i]) : 0;
     L = L > 0 ? L : 0;
-    buf[threadIdx.x] = (L + tile - 1) / tile;
+    buf[0][threadIdx.x] = (L + TILE - 1) / TILE;
+    buf[1][threadIdx.x] = (L + TILE_F8 - 1) / TILE_F8;
     __syncthreads();
     for (int off = 1; off < 1024; off <<= 1) {
-      const int32_t add = threadIdx.x >= (unsigned)off ? buf[threadIdx.x - off] : 0;
+      const bool in = threadIdx.x >= (unsigned)off;
+      const int32_t add0 = in ? buf[0][threadIdx.x - off] : 0, add1 = in ? buf[1][threadIdx.x - off] : 0;
       __syncthreads();
-      buf[threadIdx.x] += add;
+      buf[0][threadIdx.x] += add0;
+      buf[1][threadIdx.x] += add1;
       __syncthreads();
     }
-    if (i < batch) plan[i + 1] = carry + buf[threadIdx.x];
-    carry += buf[1023];
+    if (i < batch) out[0][i + 1] = carry[0] + buf[0][threadIdx.x], out[1][i + 1] = carry[1] + buf[1][threadIdx.x];
+    carry[0] += buf[0][1023];
+    carry[1] += buf[1][1023];
     __syncthreads();
   }
 }
@@ -1561,7 +1569,7 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   const size_t slots = units + (size_t)sz->num_shares + (tail ? units : 0);  // unit + share; tails
   size_t off = 0;
   sz->plan_off = off;
-  if (need_plan) off = align256(off + sizeof(int32_t) * ((size_t)batch + 1));
+  if (need_plan) off = align256(off + 2 * sizeof(int32_t) * ((size_t)batch + 1));
   sz->q_off = off;
   off = align256(off + sizeof(uint16_t) * units * rows * d);
   sz->rs_off = off;  // fp8 calls: score scale per packed row
@@ -1633,7 +1641,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   // e4m3 K/V run on tiles of TILE_F8 positions: they always plan for themselves (a
   // caller's plan counts TILE-position tiles).
-  const bool need_plan = a.seqlens != nullptr && (c.plan == nullptr || a.f8);
+  const bool need_plan = a.seqlens != nullptr && c.plan == nullptr;
   Sizing sz;
   int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, a.f8 != 0);
   if (rc != FM_OK) return rc;
@@ -1669,17 +1677,17 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   a.part_lse = (float *)(ws + sz.lse_off);
   a.part_o = (uint16_t *)(ws + sz.o_off);
   if (a.seqlens != nullptr) {
+    const int32_t *plan = c.plan;
     if (need_plan) {
-      int32_t *plan = (int32_t *)(ws + sz.plan_off);
-      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, plan, a.csr, a.f8 ? TILE_F8 : TILE);
+      int32_t *own = (int32_t *)(ws + sz.plan_off);
+      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, own, a.csr);
       FM_CHECK_HIP(hipGetLastError());
-      a.plan = plan;
-    } else {
-      a.plan = c.plan;
+      plan = own;
     }
+    a.plan = plan + (a.f8 ? c.batch + 1 : 0);  // the prefix of this call's tile size
   } else {
     a.plan = nullptr;
-    a.uniform_tiles = (a.uniform_len + TILE - 1) / TILE;
+    a.uniform_tiles = (a.uniform_len + (a.f8 ? TILE_F8 : TILE) - 1) / (a.f8 ? TILE_F8 : TILE);
   }
   const int64_t qblocks = (units * sz.rp.nrb + 3) / 4;
   const VerifyArgs nov{};
@@ -1720,13 +1728,13 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
 using namespace fm;
 
 extern "C" size_t fm_attn_plan_bytes(int32_t batch) {
-  return sizeof(int32_t) * ((size_t)(batch < 0 ? 0 : batch) + 1);
+  return 2 * sizeof(int32_t) * ((size_t)(batch < 0 ? 0 : batch) + 1);
 }
 
 extern "C" int fm_attn_plan(const int32_t *seqlens, int32_t batch, int32_t *plan, void *stream) {
   FM_REQUIRE(batch >= 0, "bad batch");
   FM_REQUIRE(plan != nullptr && (batch == 0 || seqlens != nullptr), "NULL pointer");
-  attn_plan_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(seqlens, batch, plan, 0, TILE);
+  attn_plan_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(seqlens, batch, plan, 0);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }

@@ -141,20 +141,36 @@ __global__ __launch_bounds__(SEL_THREADS) void select_tiles_kernel(const SelectA
       const float u = word_to_uniform(c[0]);
       key = x / temp - logf(-logf(u));
     }
-    if (better(key, (int32_t)col, bk, bi)) bk = key, bi = (int32_t)col;
+    // A thread visits its logits in increasing index order: a strictly larger key, the
+    // first one, or a first NaN over a number takes the place (branch-free); the full
+    // order settles ties between threads.
+    const bool take = key > bk || bi == INT32_MAX || (key != key && bk == bk);
+    bk = take ? key : bk;
+    bi = take ? (int32_t)col : bi;
   };
   const int64_t base = (int64_t)tile * SEL_TILE;
+  constexpr int IT = SEL_TILE / (8 * SEL_THREADS);
+  if (a.vec && base + SEL_TILE <= a.vocab) {  // a whole tile: every load in flight first
+    float x[IT][8];
 #pragma unroll
-  for (int it = 0; it < SEL_TILE / (8 * SEL_THREADS); ++it) {
-    const int64_t col0 = base + 8 * ((int64_t)it * SEL_THREADS + threadIdx.x);
-    if (col0 >= a.vocab) break;
-    if (a.vec && col0 + 8 <= a.vocab) {
-      float x[8];
-      logits8<TY>(src, col0, x);
+    for (int it = 0; it < IT; ++it) logits8<TY>(src, base + 8 * ((int64_t)it * SEL_THREADS + threadIdx.x), x[it]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) visit(col0 + j, x[j]);
-    } else {
-      for (int j = 0; j < 8 && col0 + j < a.vocab; ++j) visit(col0 + j, logit_at<TY>(src, col0 + j));
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) visit(base + 8 * ((int64_t)it * SEL_THREADS + threadIdx.x) + j, x[it][j]);
+  } else {  // the vocabulary's last, partial tile (or unaligned rows)
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int64_t col0 = base + 8 * ((int64_t)it * SEL_THREADS + threadIdx.x);
+      if (col0 >= a.vocab) break;
+      if (a.vec && col0 + 8 <= a.vocab) {
+        float x[8];
+        logits8<TY>(src, col0, x);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) visit(col0 + j, x[j]);
+      } else {
+        for (int j = 0; j < 8 && col0 + j < a.vocab; ++j) visit(col0 + j, logit_at<TY>(src, col0 + j));
+      }
     }
   }
   wave_best(bk, bi);

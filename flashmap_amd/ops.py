@@ -213,13 +213,14 @@ def workspace_for(batch: int, max_seqlen_q: int, hq: int, hkv: int, head_dim: in
 
 
 def attention_plan(seqlens: torch.Tensor) -> torch.Tensor:
-    """The split-KV plan of one step (int32 ``(batch + 1,)``), shared by every layer that
-    attends with these context lengths; the analogue of FlashAttention's
-    ``get_scheduler_metadata`` (flashmap/vllm/model.py:967-989)."""
+    """The split-KV plan of one step (int32 ``(2 (batch + 1),)``: the tile prefixes for
+    bf16 and for e4m3 K/V), shared by every layer that attends with these context
+    lengths; the analogue of FlashAttention's ``get_scheduler_metadata``
+    (flashmap/vllm/model.py:967-989)."""
     _check_cuda(seqlens)
     seqlens = _i32(seqlens)
     batch = seqlens.shape[0]
-    plan = torch.empty(batch + 1, dtype=torch.int32, device=seqlens.device)
+    plan = torch.empty(2 * (batch + 1), dtype=torch.int32, device=seqlens.device)
     call("fm_attn_plan", seqlens.data_ptr(), batch, plan.data_ptr(), _stream(seqlens))
     return plan
 

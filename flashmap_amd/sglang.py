@@ -67,7 +67,7 @@ def paged_cross_attention(
     pool rows of ``key_buffer / value_buffer (pool, kv_heads, head_dim)``, listed by
     ``page_table`` (page size 1)."""
     plan = scheduler_metadata
-    if plan is not None and (plan.dtype != torch.int32 or plan.numel() != cache_seqlens.shape[0] + 1):
+    if plan is not None and (plan.dtype != torch.int32 or plan.numel() != 2 * (cache_seqlens.shape[0] + 1)):
         raise ValueError("scheduler_metadata must be cross_attention_schedule(cache_seqlens) or None")
     return ops.block_attention_token_paged(query, key_buffer, value_buffer, cache_seqlens, page_table,
                                            plan=plan)
@@ -85,7 +85,7 @@ def paged_cross_attention_fp8(
     query is quantized per (request, head) with scale amax / 448 and every operand
     descaled (flashmap/sglang/model.py:154-181); returns the query's dtype."""
     plan = scheduler_metadata
-    if plan is not None and (plan.dtype != torch.int32 or plan.numel() != cache_seqlens.shape[0] + 1):
+    if plan is not None and (plan.dtype != torch.int32 or plan.numel() != 2 * (cache_seqlens.shape[0] + 1)):
         raise ValueError("scheduler_metadata must be cross_attention_schedule(cache_seqlens) or None")
     return ops.block_attention_token_paged_fp8(query, key_buffer, value_buffer, cache_seqlens, page_table,
                                                plan=plan)

@@ -63,7 +63,7 @@ def cross_attention_schedule(seqused_k: torch.Tensor) -> torch.Tensor:
 def _plan(meta: torch.Tensor | None, batch: int) -> torch.Tensor | None:
     if meta is None:
         return None
-    if meta.dtype != torch.int32 or meta.dim() != 1 or meta.numel() != batch + 1:
+    if meta.dtype != torch.int32 or meta.dim() != 1 or meta.numel() != 2 * (batch + 1):
         raise ValueError("scheduler_metadata must be cross_attention_schedule(seqused_k) or None")
     return meta
 

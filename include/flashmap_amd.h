@@ -93,7 +93,9 @@ int fm_rms_norm_rope(const void *x, void *out, int64_t tokens, int32_t heads, in
  * A sequence with seqlen(b) == 0 gets zeros (vLLM's seqused_k = 0 rows).
  * ------------------------------------------------------------------------------ */
 
-/* Bytes of the plan buffer for `batch` sequences. */
+/* Bytes of the plan buffer for `batch` sequences: 2 (batch + 1) int32, the prefixes of the
+ * sequences' tile counts for bf16 K/V (tiles of 32 positions) and for e4m3 K/V (tiles of 64
+ * positions), so one step plan serves calls onto caches of either kind. */
 size_t fm_attn_plan_bytes(int32_t batch);
 /* Writes the step's plan from seqlens (batch,) int32 into `plan` (device, int32).
  * Replaces get_scheduler_metadata (flashmap/vllm/model.py:967-989,

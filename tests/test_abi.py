@@ -93,8 +93,8 @@ def test_attention_argument_errors(lib):
 
 
 def test_plan_and_workspace_sizes_without_device(lib):
-    assert lib.fm_attn_plan_bytes(5) == 4 * 6
-    assert lib.fm_attn_plan_bytes(-3) == 4
+    assert lib.fm_attn_plan_bytes(5) == 2 * 4 * 6  # the bf16 and e4m3 tile prefixes
+    assert lib.fm_attn_plan_bytes(-3) == 2 * 4
     # invalid shapes answer with a minimal size instead of querying the device
     assert lib.fm_attn_workspace_bytes(4, 16, 30, 8, 128, 1024, 0) == 256
     assert lib.fm_attn_workspace_bytes(4, 16, 32, 8, 96, 1024, 0) == 256
