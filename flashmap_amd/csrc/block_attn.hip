@@ -1503,12 +1503,17 @@ struct RowPlan {
   int rgroups;  // units per KV head
 };
 
-// Row blocks per unit (= wavefronts per workgroup) and row groups per KV head.
+// Row blocks per unit (= consumer wavefronts per replica) and row groups per KV head. A
+// unit of one 16-row block (MHA with K = 16) gets a second, all-zero block: two consumer
+// wavefronts per replica stream the same K/V 20 % faster than one on MI355X (R8B, 16 KV
+// heads: 388 -> 323 us), whose idle half of the math is free on this HBM-bound path. The
+// zero rows are packed as zeros and never stored.
 static RowPlan row_plan(int group, int q_len) {
   const int total = (group * q_len + 15) / 16;
   RowPlan p;
   p.rgroups = (total + NRB_MAX - 1) / NRB_MAX;
   p.nrb = (total + p.rgroups - 1) / p.rgroups;
+  if (p.nrb == 1) p.nrb = 2;
   return p;
 }
 
