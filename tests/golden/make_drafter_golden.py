@@ -2,7 +2,7 @@
 drafter's ``draft`` on two tiny random-init configurations, the composition that no
 closed form pins (AdaLN-zero ordering, gated residuals, time conditioning, state mixing,
 the jump loop). Run once, in the development container where the reference source is
-present (never on the GPU box, and never as part of the tests):
+present (never where the GPU tests run, and never as part of the tests):
 
     python tests/golden/make_drafter_golden.py /root/reference
 
