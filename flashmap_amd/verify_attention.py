@@ -14,7 +14,7 @@ and runs ``fm_verify_attention``:
 
 Only shapes are read on the host, so a call can be captured in a graph. A case the
 kernels do not handle returns False having done nothing (the caller then runs
-extend_attention_fwd), exactly where the reference's does, plus where this build's
+extend_attention_fwd), exactly where the reference's does, plus where the gfx950
 kernels need bf16 and head_dim 64 or 128.
 """
 
@@ -107,7 +107,7 @@ class SplitKVVerify:
         h_kv, dv = k_buffer.shape[1], v_buffer.shape[-1]
         if bs < 1 or q.shape[0] != bs * length or h_q % h_kv or k_buffer.dtype != q.dtype:
             return False
-        # This build's kernels: bf16, head_dim 64 / 128, values as wide as keys, pool
+        # The gfx950 kernels: bf16, head_dim 64 / 128, values as wide as keys, pool
         # and output rows readable and writable in place.
         if q.dtype != torch.bfloat16 or d not in (64, 128) or dv != d or v_buffer.dtype != q.dtype:
             return False
