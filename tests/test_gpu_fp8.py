@@ -90,7 +90,8 @@ def _e4m3(shape, g, scale=1.0):
     return ref.to_e4m3(torch.randn(*shape, generator=g) * scale)
 
 
-@pytest.mark.parametrize("page,d,hq,hkv", [(16, 128, 32, 8), (8, 64, 8, 2), (16, 128, 16, 16), (32, 64, 40, 8)])
+@pytest.mark.parametrize("page,d,hq,hkv", [(16, 128, 32, 8), (8, 64, 8, 2), (16, 128, 16, 16), (32, 64, 40, 8),
+                                         (16, 128, 48, 8), (8, 128, 24, 4)])
 def test_paged_fp8_attention_descales(dev, page, d, hq, hkv):
     print(f"fp8 paged page={page} d={d} hq={hq} hkv={hkv}", flush=True)
     g = gen(60 + page + d + hq)
@@ -183,3 +184,4 @@ def test_paged_fp8_large_batch(dev):
                                           k_rows, 80, d ** -0.5)
     torch.cuda.synchronize()
     check_close(got.cpu().float(), ref.block_attention_paged_vllm_fp8(q8, cache, cu, lens, bt, d ** -0.5))
+
