@@ -91,7 +91,8 @@ def rms_norm_rope_vllm(x, weight, cos_sin, positions, eps):
 
 def rms_norm_rope_sglang(x, weight, freqs, eps):
     """flashmap_sglang::rms_norm_rope on ``x (..., T, H, D)`` with one table row per
-    token ``freqs (..., T, D/2, 2)`` (flashmap/sglang/kernels.py:149-189)."""
+    token ``freqs (..., T, D/2, 2)`` (flashmap/sglang/kernels.py:149-189). Pinned by: equal to rms_norm_rope_vllm on the same rows with
+    the vLLM table layout (test_oracle_norm)."""
     cos, sin = freqs[..., 0].unsqueeze(-2), freqs[..., 1].unsqueeze(-2)
     return apply_rope(rms_norm(x, weight, eps), cos, sin)
 
@@ -152,7 +153,8 @@ def block_attention_contig(query, keys, values, seqlens_k=None, scale=None):
     """a5: ``query (B, T, Hq, D)`` onto FlashMapCache views ``keys/values (B, Hkv, L, D)``,
     sequence b reading its first ``seqlens_k[b]`` positions (all L by default)
     (flashmap/modeling_flashmap.py:144-147, 218-219). Returns float32 (B, T, Hq, D);
-    zeros for an empty context."""
+    zeros for an empty context. Pinned by: its attention core against float64 brute force,
+    seqlens truncation and empty contexts (test_oracle_attention)."""
     b_, t_, hq, d = query.shape
     out = torch.zeros((b_, t_, hq, d))
     for b in range(b_):
@@ -178,7 +180,8 @@ def vllm_gather_slots(block_table: np.ndarray, seqlen: int, page_size: int, b: i
 def gather_vllm(kv_cache: torch.Tensor, block_table, seqlen: int, b: int):
     """K and V ``(Hkv, seqlen, D)`` of request ``b`` from a vLLM cache
     ``(num_blocks, Hkv, page, 2D)`` whose rows hold K then V
-    (flashmap/vllm/model.py:107-112: ``kv_cache.transpose(1, 2).split(D, -1)``)."""
+    (flashmap/vllm/model.py:107-112: ``kv_cache.transpose(1, 2).split(D, -1)``). Pinned by: the gather closed form and paged == contiguous under
+    block permutations (test_oracle_attention)."""
     d = kv_cache.shape[-1] // 2
     page = kv_cache.shape[2]
     idx = vllm_gather_slots(np.asarray(block_table), seqlen, page, b)
@@ -190,7 +193,8 @@ def block_attention_paged_vllm(query, kv_cache, cu_seqlens_q, seqused_k, block_t
     """a6: flashmap_vllm::paged_cross_attention (flashmap/vllm/model.py:93-134):
     request b's query rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` of ``query (tokens,
     Hq, D)`` attend non-causally to its first ``seqused_k[b]`` paged positions.
-    Returns float32 (tokens, Hq, D), zeros for empty contexts."""
+    Returns float32 (tokens, Hq, D), zeros for empty contexts. Pinned by: equal to block_attention_contig under
+    any block permutation (test_oracle_attention)."""
     out = torch.zeros(query.shape)
     bt = np.asarray(block_table)
     for b in range(len(seqused_k)):
@@ -206,7 +210,8 @@ def block_attention_paged_vllm(query, kv_cache, cu_seqlens_q, seqused_k, block_t
 def block_attention_token_paged(query, key_buffer, value_buffer, cache_seqlens, page_table, scale=None):
     """a7: flashmap_sglang::paged_cross_attention (flashmap/sglang/model.py:127-146):
     request b (``query (bs, T, Hq, D)``) reads pool rows ``page_table[b, :cache_seqlens[b]]``
-    of ``key_buffer/value_buffer (pool, Hkv, D)``. Returns float32 (bs, T, Hq, D)."""
+    of ``key_buffer/value_buffer (pool, Hkv, D)``. Returns float32 (bs, T, Hq, D). Pinned by: equal to block_attention_contig on the
+    same K/V at shuffled pool slots (test_oracle_attention)."""
     out = torch.zeros(query.shape)
     for b in range(query.shape[0]):
         n = int(cache_seqlens[b])
@@ -308,7 +313,8 @@ def block_self_attention(qkv, q_norm, k_norm, cos, sin, eps, scale=None):
 def project_keys(k_rows, k_norm_w, cos, sin, eps):
     """The K side of the prologue: ``apply_rope(k_norm(k))`` of ``k_rows (..., H, D)``
     with ``cos/sin`` broadcastable to ``(..., 1, D/2)`` (flashmap/modeling_flashmap.py:139-142;
-    flashmap/vllm/kernels.py:276-290)."""
+    flashmap/vllm/kernels.py:276-290). Pinned by: composition of rms_norm and apply_rope, each pinned
+    (test_oracle_norm, test_oracle_rope)."""
     return apply_rope(rms_norm(k_rows, k_norm_w, eps), cos, sin)
 
 
@@ -395,7 +401,8 @@ def to_e4m3(x: torch.Tensor) -> torch.Tensor:
 def rotate_f32(y: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """Interleaved-pair RoPE of ``y`` in float32 without the final rounding (the fp8
     writers quantize the rotated keys directly: flashmap/vllm/kernels.py:287-296,
-    flashmap/sglang/kernels.py:330-331)."""
+    flashmap/sglang/kernels.py:330-331). Pinned by: its result rounded
+    to bf16 equals apply_rope (test_oracle_rope), and float64 on the same pairs."""
     e, o = y[..., 0::2].float(), y[..., 1::2].float()
     out = torch.empty(y.shape, dtype=torch.float32)
     out[..., 0::2] = e * cos - o * sin
@@ -534,7 +541,8 @@ def write_context_kv_pool(kv, k_bufs, v_bufs, k_norm, cos_sin_cat, positions, lo
     calls it, interleaved RoPE; the reference's rounding of the norm, scale rounded to
     bf16 first, flashmap/modeling_flashmap.py:79-80): ``kv (tokens, L*2*kv_size)``,
     per layer keys then values; token t goes to pool row ``locs[t]`` unless negative or
-    past its request's ``commit_lens`` column."""
+    past its request's ``commit_lens`` column. Pinned by: write then read back equals project_keys
+    / the values at committed slots, uncommitted tokens untouched (test_oracle_layouts)."""
     heads = kv_size // head_dim
     half = head_dim // 2
     rows = cos_sin_cat[positions.long()]

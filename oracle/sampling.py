@@ -34,7 +34,7 @@ TWO_PI = np.float32(6.283185307179586)
 def philox4x32(c0, c1, c2, c3, k0, k1, rounds: int = 10):
     """Philox-4x32 on uint32 arrays (broadcast): per round
     ``(c0, c1, c2, c3) <- (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0))``,
-    then the key gains the Weyl increments (triton/language/random.py: philox_impl)."""
+    then the key gains the Weyl increments (triton/language/random.py: philox_impl). Pinned by: the Random123 known-answer vectors."""
     c0, c1, c2, c3 = (np.asarray(x, dtype=np.uint32) for x in (c0, c1, c2, c3))
     k0, k1 = np.asarray(k0, dtype=np.uint32), np.asarray(k1, dtype=np.uint32)
     for _ in range(rounds):
@@ -58,7 +58,8 @@ def _seed_words(seed):
 def randint4x(seed, offset, wide: bool = False):
     """The four words for int64 ``seed`` and integer ``offset`` arrays: counter = (offset's
     low word, its high word if the offsets are 64-bit (``wide``) else 0, 0, 0). Both
-    reference kernels pass int32 offsets."""
+    reference kernels pass int32 offsets. Pinned by: the counter and key words of a known-answer
+    vector (test_counter_and_key_words)."""
     off = np.asarray(offset).astype(np.int64).astype(np.uint64)
     k0, k1 = _seed_words(seed)
     zero = np.zeros(off.shape, dtype=np.uint32)
@@ -67,17 +68,21 @@ def randint4x(seed, offset, wide: bool = False):
 
 
 def uniform(x):
-    """uint32 words -> float32 in [0, 1): the word as int32, negatives folded by -x - 1."""
+    """uint32 words -> float32 in [0, 1): the word as int32, negatives folded by -x - 1. Pinned by: its end points (0, -1, INT_MAX, INT_MIN) and range."""
     i = np.asarray(x, dtype=np.uint32).view(np.int32).astype(np.int64)
     i = np.where(i < 0, -i - 1, i)
     return i.astype(np.float32) * UNIFORM_SCALE
 
 
 def rand(seed, offset):
+    """``tl.rand``: the uniform of the first word. Pinned by: range and moments over 200000
+    offsets (test_uniform_map)."""
     return uniform(randint4x(seed, offset)[0])
 
 
 def randn(seed, offset):
+    """``tl.randn``: Box-Muller of the first two words' uniforms. Pinned by: moments, and
+    the same words in float64 (test_normals_moments_and_box_muller)."""
     w = randint4x(seed, offset)
     u1, u2 = uniform(w[0]), uniform(w[1])
     u1 = np.maximum(np.float32(1e-7), u1)
@@ -89,7 +94,9 @@ def randn(seed, offset):
 def seeded_normal(seeds, rows, positions, n_cols: int, scale: float = 1.0):
     """flashmap/vllm/kernels.py:367-410: row ``i`` of ``(len(rows), n_cols)`` float32
     standard normals times ``scale``, keyed by ``seeds[rows[i]] * 1000003 + positions[i]``
-    (int64, wrapping; seed 0 where ``rows[i] < 0``), column ``j`` at offset ``j``."""
+    (int64, wrapping; seed 0 where ``rows[i] < 0``), column ``j`` at offset ``j``. Pinned
+    by: each row against randn at the key computed in Python integers modulo 2^64
+    (test_seeded_normal_keys)."""
     seeds = np.asarray(seeds, dtype=np.int64)
     rows = np.asarray(rows).astype(np.int64)
     pos = np.asarray(positions).astype(np.int64)
@@ -103,7 +110,8 @@ def seeded_normal(seeds, rows, positions, n_cols: int, scale: float = 1.0):
 
 def argmax_first(x):
     """Per row, the index of the largest value, the first among equals (torch.argmax's
-    rule; a NaN counts as the largest, the first NaN wins)."""
+    rule; a NaN counts as the largest, the first NaN wins). Pinned by: hand-checked rows
+    (ties, -inf, NaN) (test_argmax_rule)."""
     x = np.asarray(x, dtype=np.float32)
     nan = np.isnan(x)
     idx = np.argmax(np.where(nan, -np.inf, x), axis=-1)
@@ -113,7 +121,7 @@ def argmax_first(x):
 
 def split_argmax(logits):
     """flashmap/vllm/fold.py:117-128: ``logits.argmax(-1)`` (chunked on the GPU; the chunks
-    do not change the result)."""
+    do not change the result). Pinned by: argmax_first."""
     return argmax_first(logits)
 
 
@@ -121,7 +129,8 @@ def sample_keys(logits, temperatures, greedy, seed: int, row0: int = 0):
     """The keys flashmap/sglang/kernels.py:195-247 takes the argmax of, for rows
     ``row0 ..`` of the batch: a greedy row's key is its logit (float32), another row's
     ``logit / T - log(-log(u))`` with ``u = rand(seed, row * V + col)``, the offset in int32
-    arithmetic as the reference's kernel forms it (low word, high word 0)."""
+    arithmetic as the reference's kernel forms it (low word, high word 0). Pinned by: the sampler's
+    frequencies against softmax(logits / T) (chi-square) and its greedy rows."""
     x = np.asarray(logits, dtype=np.float32)
     rows, vocab = x.shape
     t = np.asarray(temperatures, dtype=np.float32)
@@ -136,5 +145,5 @@ def sample_keys(logits, temperatures, greedy, seed: int, row0: int = 0):
 def sample_rows(logits, temperatures, greedy, seed: int, row0: int = 0):
     """flashmap/sglang/kernels.py:195-247: per row, the argmax of :func:`sample_keys`, the
     first index among equals (Gumbel-max: a sample of softmax(logits / T) for the
-    non-greedy rows)."""
+    non-greedy rows). Pinned by: as sample_keys."""
     return argmax_first(sample_keys(logits, temperatures, greedy, seed, row0))

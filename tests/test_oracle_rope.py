@@ -108,3 +108,19 @@ def test_rope_descriptors_address_the_tables():
             j = r * desc.row_stride + i * desc.pair_stride
             assert ctypes.c_float.from_address(cbase + 4 * j).value == table[r, i, 0].item()
             assert ctypes.c_float.from_address(desc.sin_ptr + 4 * j).value == table[r, i, 1].item()
+
+
+def test_rotation_without_rounding_rounds_to_apply_rope():
+    """rotate_f32 (the fp8 writers' unrounded rotation) is apply_rope before its rounding,
+    and agrees with float64 on the same pairs."""
+    g = torch.Generator().manual_seed(9)
+    y = torch.randn(5, 3, 64, generator=g).bfloat16()
+    ang = torch.rand(5, 1, 32, generator=g) * 6.3
+    cos, sin = ang.cos(), ang.sin()
+    got = ref.rotate_f32(y, cos, sin)
+    assert got.dtype == torch.float32
+    assert torch.equal(got.bfloat16(), ref.apply_rope(y, cos, sin))
+    e, o = y[..., 0::2].double(), y[..., 1::2].double()
+    c, s = cos.double(), sin.double()
+    assert torch.allclose(got[..., 0::2].double(), e * c - o * s, atol=1e-5)
+    assert torch.allclose(got[..., 1::2].double(), o * c + e * s, atol=1e-5)
