@@ -180,8 +180,9 @@ def vllm_gather_slots(block_table: np.ndarray, seqlen: int, page_size: int, b: i
 def gather_vllm(kv_cache: torch.Tensor, block_table, seqlen: int, b: int):
     """K and V ``(Hkv, seqlen, D)`` of request ``b`` from a vLLM cache
     ``(num_blocks, Hkv, page, 2D)`` whose rows hold K then V
-    (flashmap/vllm/model.py:107-112: ``kv_cache.transpose(1, 2).split(D, -1)``). Pinned by: the gather closed form and paged == contiguous under
-    block permutations (test_oracle_attention)."""
+    (flashmap/vllm/model.py:107-112: ``kv_cache.transpose(1, 2).split(D, -1)``). Pinned
+    by: the gather closed form and paged == contiguous under block permutations
+    (test_oracle_attention)."""
     d = kv_cache.shape[-1] // 2
     page = kv_cache.shape[2]
     idx = vllm_gather_slots(np.asarray(block_table), seqlen, page, b)
