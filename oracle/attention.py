@@ -90,9 +90,9 @@ def rms_norm_rope_vllm(x, weight, cos_sin, positions, eps):
 
 
 def rms_norm_rope_sglang(x, weight, freqs, eps):
-    """flashmap_sglang::rms_norm_rope on ``x (..., T, H, D)`` with one table row per
-    token ``freqs (..., T, D/2, 2)`` (flashmap/sglang/kernels.py:149-189). Pinned by: equal to rms_norm_rope_vllm on the same rows with
-    the vLLM table layout (test_oracle_norm)."""
+    """flashmap_sglang::rms_norm_rope on ``x (..., T, H, D)`` with one table row per token
+    ``freqs (..., T, D/2, 2)`` (flashmap/sglang/kernels.py:149-189). Pinned by: equal to
+    rms_norm_rope_vllm on the same rows with the vLLM table layout (test_oracle_norm)."""
     cos, sin = freqs[..., 0].unsqueeze(-2), freqs[..., 1].unsqueeze(-2)
     return apply_rope(rms_norm(x, weight, eps), cos, sin)
 
@@ -191,11 +191,11 @@ def gather_vllm(kv_cache: torch.Tensor, block_table, seqlen: int, b: int):
 
 
 def block_attention_paged_vllm(query, kv_cache, cu_seqlens_q, seqused_k, block_table, scale=None):
-    """a6: flashmap_vllm::paged_cross_attention (flashmap/vllm/model.py:93-134):
-    request b's query rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` of ``query (tokens,
-    Hq, D)`` attend non-causally to its first ``seqused_k[b]`` paged positions.
-    Returns float32 (tokens, Hq, D), zeros for empty contexts. Pinned by: equal to block_attention_contig under
-    any block permutation (test_oracle_attention)."""
+    """a6: flashmap_vllm::paged_cross_attention (flashmap/vllm/model.py:93-134): request b's
+    query rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` of ``query (tokens, Hq, D)`` attend
+    non-causally to its first ``seqused_k[b]`` paged positions. Returns float32 (tokens, Hq,
+    D), zeros for empty contexts. Pinned by: equal to block_attention_contig under any block
+    permutation (test_oracle_attention)."""
     out = torch.zeros(query.shape)
     bt = np.asarray(block_table)
     for b in range(len(seqused_k)):
@@ -209,10 +209,11 @@ def block_attention_paged_vllm(query, kv_cache, cu_seqlens_q, seqused_k, block_t
 
 
 def block_attention_token_paged(query, key_buffer, value_buffer, cache_seqlens, page_table, scale=None):
-    """a7: flashmap_sglang::paged_cross_attention (flashmap/sglang/model.py:127-146):
-    request b (``query (bs, T, Hq, D)``) reads pool rows ``page_table[b, :cache_seqlens[b]]``
-    of ``key_buffer/value_buffer (pool, Hkv, D)``. Returns float32 (bs, T, Hq, D). Pinned by: equal to block_attention_contig on the
-    same K/V at shuffled pool slots (test_oracle_attention)."""
+    """a7: flashmap_sglang::paged_cross_attention (flashmap/sglang/model.py:127-146): request b
+    (``query (bs, T, Hq, D)``) reads pool rows ``page_table[b, :cache_seqlens[b]]`` of
+    ``key_buffer/value_buffer (pool, Hkv, D)``. Returns float32 (bs, T, Hq, D). Pinned by:
+    equal to block_attention_contig on the same K/V at shuffled pool slots
+    (test_oracle_attention)."""
     out = torch.zeros(query.shape)
     for b in range(query.shape[0]):
         n = int(cache_seqlens[b])
@@ -312,10 +313,10 @@ def block_self_attention(qkv, q_norm, k_norm, cos, sin, eps, scale=None):
 
 
 def project_keys(k_rows, k_norm_w, cos, sin, eps):
-    """The K side of the prologue: ``apply_rope(k_norm(k))`` of ``k_rows (..., H, D)``
-    with ``cos/sin`` broadcastable to ``(..., 1, D/2)`` (flashmap/modeling_flashmap.py:139-142;
-    flashmap/vllm/kernels.py:276-290). Pinned by: composition of rms_norm and apply_rope, each pinned
-    (test_oracle_norm, test_oracle_rope)."""
+    """The K side of the prologue: ``apply_rope(k_norm(k))`` of ``k_rows (..., H, D)`` with
+    ``cos/sin`` broadcastable to ``(..., 1, D/2)`` (flashmap/modeling_flashmap.py:139-142;
+    flashmap/vllm/kernels.py:276-290). Pinned by: composition of rms_norm and apply_rope,
+    each pinned (test_oracle_norm, test_oracle_rope)."""
     return apply_rope(rms_norm(k_rows, k_norm_w, eps), cos, sin)
 
 

@@ -34,7 +34,8 @@ TWO_PI = np.float32(6.283185307179586)
 def philox4x32(c0, c1, c2, c3, k0, k1, rounds: int = 10):
     """Philox-4x32 on uint32 arrays (broadcast): per round
     ``(c0, c1, c2, c3) <- (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0))``,
-    then the key gains the Weyl increments (triton/language/random.py: philox_impl). Pinned by: the Random123 known-answer vectors."""
+    then the key gains the Weyl increments (triton/language/random.py: philox_impl).
+    Pinned by: the Random123 known-answer vectors."""
     c0, c1, c2, c3 = (np.asarray(x, dtype=np.uint32) for x in (c0, c1, c2, c3))
     k0, k1 = np.asarray(k0, dtype=np.uint32), np.asarray(k1, dtype=np.uint32)
     for _ in range(rounds):
@@ -68,7 +69,8 @@ def randint4x(seed, offset, wide: bool = False):
 
 
 def uniform(x):
-    """uint32 words -> float32 in [0, 1): the word as int32, negatives folded by -x - 1. Pinned by: its end points (0, -1, INT_MAX, INT_MIN) and range."""
+    """uint32 words -> float32 in [0, 1): the word as int32, negatives folded by -x - 1. Pinned
+    by: its end points (0, -1, INT_MAX, INT_MIN) and range."""
     i = np.asarray(x, dtype=np.uint32).view(np.int32).astype(np.int64)
     i = np.where(i < 0, -i - 1, i)
     return i.astype(np.float32) * UNIFORM_SCALE
