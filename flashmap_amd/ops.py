@@ -87,6 +87,20 @@ def _i32(t: torch.Tensor) -> torch.Tensor:
     return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
 
 
+def _need_rows(t: torch.Tensor | None, n: int, what: str) -> None:
+    """Raise unless ``t`` has at least ``n`` entries along its first dimension: the
+    kernels index it that far without bounds checks."""
+    have = None if t is None else (t.shape[0] if t.dim() else 0)
+    if have is not None and have < n:
+        raise ValueError(f"{what} has {have} rows; the call reads {n}")
+
+
+def _need_numel(t: torch.Tensor | None, n: int, what: str) -> None:
+    """Raise unless ``t`` holds at least ``n`` values (read flat by the kernels)."""
+    if t is not None and t.numel() < n:
+        raise ValueError(f"{what} holds {t.numel()} values; the call reads {n}")
+
+
 # ---------------------------------------------------------------------------- rope
 
 
@@ -100,10 +114,18 @@ class Rope:
     row_stride: int
     pair_stride: int
     rows: int
+    pairs: int
     keep: tuple = ()
 
     def args(self) -> list:
         return [self.cos.data_ptr(), self.sin_ptr, self.row_stride, self.pair_stride, self.rows]
+
+    def check(self, head_dim: int) -> None:
+        """The kernels read pairs ``[0, head_dim / 2)`` of rows ``[0, rows)`` (positions
+        are clamped to the rows)."""
+        if 2 * self.pairs != head_dim or self.rows < 1:
+            raise ValueError(f"rotary table of {self.rows} rows x {self.pairs} pairs does not serve "
+                             f"head_dim {head_dim}")
 
 
 def rope_from_table(cos_sin: torch.Tensor) -> Rope:
@@ -112,25 +134,29 @@ def rope_from_table(cos_sin: torch.Tensor) -> Rope:
     flashmap/sglang/model.py:116-123). Rows are the leading dims flattened."""
     if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous() or cos_sin.shape[-1] != 2:
         raise ValueError("rotary table must be contiguous float32 (..., head_dim/2, 2)")
-    half = cos_sin.shape[-2]
-    return Rope(cos_sin, cos_sin.data_ptr() + 4, 2 * half, 2, max(cos_sin.numel() // (2 * half), 1), (cos_sin,))
+    half = cos_sin.shape[-2] if cos_sin.dim() >= 2 else 0
+    rows = cos_sin.numel() // (2 * half) if half else 0
+    return Rope(cos_sin, cos_sin.data_ptr() + 4, 2 * half, 2, rows, half, (cos_sin,))
 
 
 def rope_from_split(cos: torch.Tensor, sin: torch.Tensor) -> Rope:
     """transformers' ``rope_tables``: separate ``cos`` and ``sin`` ``(..., D/2)``
     (flashmap/modeling_flashmap.py:53-58)."""
+    if cos.shape != sin.shape or cos.dim() == 0:
+        raise ValueError(f"cos and sin tables must share one shape (..., head_dim/2), got "
+                         f"{tuple(cos.shape)} and {tuple(sin.shape)}")
     cos, sin = _f32(cos), _f32(sin)
     half = cos.shape[-1]
-    return Rope(cos, sin.data_ptr(), half, 1, max(cos.numel() // half, 1), (cos, sin))
+    return Rope(cos, sin.data_ptr(), half, 1, cos.numel() // half if half else 0, half, (cos, sin))
 
 
 def rope_from_cat(table: torch.Tensor) -> Rope:
     """SGLang's writer table ``(P, D)`` = ``[cos(D/2) | sin(D/2)]`` per row
     (flashmap/sglang/model.py:814-817)."""
-    if table.dtype != torch.float32 or not table.is_contiguous():
+    if table.dtype != torch.float32 or not table.is_contiguous() or table.dim() == 0:
         raise ValueError("rotary table must be contiguous float32 (P, head_dim)")
     d = table.shape[-1]
-    return Rope(table, table.data_ptr() + 4 * (d // 2), d, 1, table.numel() // d, (table,))
+    return Rope(table, table.data_ptr() + 4 * (d // 2), d, 1, table.numel() // d if d else 0, d // 2, (table,))
 
 
 # ------------------------------------------------------------------------ prologue
@@ -151,6 +177,9 @@ def rms_norm_rope(
     _check_cuda(x, weight, rope.cos, positions)
     x = _bf16_rows(x, "x")
     tokens, heads, head_dim = x.shape
+    rope.check(head_dim)
+    _need_numel(weight, head_dim, "weight")
+    _need_rows(positions, tokens, "positions")
     if out is None:
         out = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=x.device)
     if tokens == 0:
@@ -239,8 +268,39 @@ class Prologue:
         self._keep = (w, None if self.positions is None else _i64(self.positions))
         return [w.data_ptr(), *self.rope.args(), _ptr(self._keep[1]), float(self.eps)]
 
+    def check(self, tokens: int, head_dim: int) -> None:
+        """Extents the kernels rely on: ``head_dim`` weights, the table's pairs, one
+        position per query row."""
+        self.rope.check(head_dim)
+        if self.weight.numel() < head_dim:
+            raise ValueError(f"q_norm weight holds {self.weight.numel()} values, head_dim is {head_dim}")
+        _need_rows(self.positions, tokens, "prologue positions")
+
 
 _NO_PROLOGUE = [None, None, None, 0, 0, 0, None, 0.0]
+
+
+def _prologue_args(prologue: Prologue | None, tokens: int, head_dim: int) -> list:
+    if prologue is None:
+        return _NO_PROLOGUE
+    prologue.check(tokens, head_dim)
+    return prologue.args()
+
+
+def _check_requests(batch: int, cu_seqlens_q: torch.Tensor | None, tokens: int, max_seqlen_q: int,
+                    table: torch.Tensor, table_name: str, plan: torch.Tensor | None) -> None:
+    """Extents of a call's per-request tensors (the kernels index them by request
+    without bounds checks; the table's columns and the cache's pages are clamped)."""
+    if cu_seqlens_q is None:
+        if tokens < batch * max_seqlen_q:
+            raise ValueError(f"without cu_seqlens_q the query holds batch x max_seqlen_q = "
+                             f"{batch * max_seqlen_q} rows; got {tokens}")
+    else:
+        _need_rows(cu_seqlens_q, batch + 1, "cu_seqlens_q")
+    if table.dim() != 2:
+        raise ValueError(f"{table_name} must be (requests, columns), got {tuple(table.shape)}")
+    _need_rows(table, batch, table_name)
+    _need_rows(plan, 2 * (batch + 1), "plan")
 MAX_RUNS = 8  # runs of KV heads per fm_block_attn_paged_runs call
 
 
@@ -272,6 +332,11 @@ def block_attention_contig(
     ``seqlens_k (B,)`` limits each sequence to its first positions (default all L)."""
     _check_cuda(query, keys, values, seqlens_k)
     batch, q_len, hq, d = query.shape
+    if keys.dim() != 4 or keys.shape != values.shape or keys.shape[0] < batch or keys.shape[3] != d:
+        raise ValueError(f"keys and values must both be (batch >= {batch}, kv_heads, positions, {d}); got "
+                         f"{tuple(keys.shape)} and {tuple(values.shape)}")
+    _need_rows(seqlens_k, batch, "seqlens_k")
+    _need_rows(plan, 2 * (batch + 1), "plan")
     _, hkv, kv_len, _ = keys.shape
     keys, values = _bf16_rows(keys, "keys"), _bf16_rows(values, "values")
     query, out, qs, os_ = _q_out(query, out, varlen=False)
@@ -286,7 +351,7 @@ def block_attention_contig(
         keys.data_ptr(), keys.stride(0), keys.stride(1), keys.stride(2),
         values.data_ptr(), values.stride(0), values.stride(1), values.stride(2),
         _ptr(sl), kv_len, batch, q_len, hq, hkv, d, float(scale),
-        *(prologue.args() if prologue else _NO_PROLOGUE),
+        *_prologue_args(prologue, batch * q_len, d),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
     )
     return out
@@ -319,6 +384,7 @@ def block_attention_paged(
     if kv_cache.stride(-1) != 1:
         raise ValueError("kv_cache must have unit channel stride")
     batch = seqused_k.shape[0]
+    _check_requests(batch, cu_seqlens_q, tokens, max_seqlen_q, block_table, "block_table", plan)
     query, out, qs, os_ = _q_out(query, out, varlen=True)
     if batch == 0 or tokens == 0:
         return out
@@ -334,7 +400,7 @@ def block_attention_paged(
         kv_cache.data_ptr(), num_blocks, kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), d, page,
         bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
         hq, hkv, d, float(softmax_scale),
-        *(prologue.args() if prologue else _NO_PROLOGUE),
+        *_prologue_args(prologue, tokens, d),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
     )
     return out
@@ -386,6 +452,7 @@ def block_attention_paged_runs(
         raise ValueError("kv caches must have unit channel stride")
     _check_cuda(query, c0, cu_seqlens_q, seqused_k, block_table)
     batch = seqused_k.shape[0]
+    _check_requests(batch, cu_seqlens_q, tokens, max_seqlen_q, block_table, "block_table", plan)
     query, out, qs, os_ = _q_out(query, out, varlen=True)
     if batch == 0 or tokens == 0:
         return out
@@ -406,7 +473,7 @@ def block_attention_paged_runs(
         num_blocks, c0.stride(0), c0.stride(1), c0.stride(2), d, page,
         bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
         hq, hkv, d, float(softmax_scale),
-        *(prologue.args() if prologue else _NO_PROLOGUE),
+        *_prologue_args(prologue, tokens, d),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
     )
     return out
@@ -429,6 +496,11 @@ def block_attention_token_paged(
     ``page_table[b, :cache_seqlens[b]]`` (flashmap/sglang/model.py:127-146)."""
     _check_cuda(query, key_buffer, value_buffer, cache_seqlens, page_table)
     batch, q_len, hq, d = query.shape
+    if key_buffer.dim() != 3 or key_buffer.shape != value_buffer.shape or key_buffer.shape[2] != d:
+        raise ValueError(f"key_buffer and value_buffer must both be (pool, kv_heads, {d}); got "
+                         f"{tuple(key_buffer.shape)} and {tuple(value_buffer.shape)}")
+    _need_rows(cache_seqlens, batch, "cache_seqlens")
+    _check_requests(batch, None, batch * q_len, q_len, page_table, "page_table", plan)
     pool, hkv, _ = key_buffer.shape
     key_buffer, value_buffer = _bf16_rows(key_buffer, "key_buffer"), _bf16_rows(value_buffer, "value_buffer")
     query, out, qs, os_ = _q_out(query, out, varlen=False)
@@ -446,7 +518,7 @@ def block_attention_token_paged(
         key_buffer.stride(0), key_buffer.stride(1), value_buffer.stride(0), value_buffer.stride(1),
         pt.data_ptr(), pt.stride(0), pt.shape[1], sl.data_ptr(), batch, q_len, max_k,
         hq, hkv, d, float(scale),
-        *(prologue.args() if prologue else _NO_PROLOGUE),
+        *_prologue_args(prologue, batch * q_len, d),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
     )
     return out
@@ -472,11 +544,13 @@ def _fp8_query(query: torch.Tensor, out: torch.Tensor | None, varlen: bool):
     return q, out, qs, os_, 0
 
 
-def _descale_args(descales: torch.Tensor | None) -> list:
+def _descale_args(descales: torch.Tensor | None, batch: int, hkv: int) -> list:
     """(pointer, kind, batch, head strides) of FlashAttention-style descales (3, batch,
     kv_heads) float32 (expanded views allowed)."""
     if descales is None:
         return [None, 0, 0, 0]
+    if descales.dim() != 3 or descales.shape[0] < 3 or descales.shape[1] < batch or descales.shape[2] < hkv:
+        raise ValueError(f"descales must be (3, {batch}, {hkv}) (query, key, value); got {tuple(descales.shape)}")
     d = descales if descales.dtype == torch.float32 else descales.float()
     return [d.data_ptr(), d.stride(0), d.stride(1), d.stride(2)]
 
@@ -507,6 +581,7 @@ def block_attention_paged_fp8(
     if two_d != 2 * d or kv_cache.stride(-1) != 1:
         raise ValueError(f"kv_cache must be (blocks, heads, page, 2 * {d}) with unit channel stride")
     batch = seqused_k.shape[0]
+    _check_requests(batch, cu_seqlens_q, tokens, max_seqlen_q, block_table, "block_table", plan)
     query, out, qs, os_, q_fp8 = _fp8_query(query, out, varlen=True)
     if batch == 0 or tokens == 0:
         return out
@@ -521,8 +596,8 @@ def block_attention_paged_fp8(
         query.data_ptr(), q_fp8, *qs, out.data_ptr(), *os_, _ptr(cu),
         kv_cache.data_ptr(), num_blocks, kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), d, page,
         bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
-        hq, hkv, d, float(softmax_scale), *_descale_args(descales),
-        *(prologue.args() if prologue else _NO_PROLOGUE),
+        hq, hkv, d, float(softmax_scale), *_descale_args(descales, batch, hkv),
+        *_prologue_args(prologue, tokens, d),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
     )
     return out
@@ -549,6 +624,11 @@ def block_attention_token_paged_fp8(
     _fp8_cache(key_buffer, "key_buffer")
     _fp8_cache(value_buffer, "value_buffer")
     batch, q_len, hq, d = query.shape
+    if key_buffer.dim() != 3 or key_buffer.shape != value_buffer.shape or key_buffer.shape[2] != d:
+        raise ValueError(f"key_buffer and value_buffer must both be (pool, kv_heads, {d}); got "
+                         f"{tuple(key_buffer.shape)} and {tuple(value_buffer.shape)}")
+    _need_rows(cache_seqlens, batch, "cache_seqlens")
+    _check_requests(batch, None, batch * q_len, q_len, page_table, "page_table", plan)
     pool, hkv, _ = key_buffer.shape
     query, out, qs, os_, q_fp8 = _fp8_query(query, out, varlen=False)
     if batch == 0 or q_len == 0:
@@ -564,8 +644,8 @@ def block_attention_token_paged_fp8(
         key_buffer.data_ptr(), value_buffer.data_ptr(), pool,
         key_buffer.stride(0), key_buffer.stride(1), value_buffer.stride(0), value_buffer.stride(1),
         pt.data_ptr(), pt.stride(0), pt.shape[1], sl.data_ptr(), batch, q_len, max_k,
-        hq, hkv, d, float(scale), *_descale_args(descales),
-        *(prologue.args() if prologue else _NO_PROLOGUE),
+        hq, hkv, d, float(scale), *_descale_args(descales, batch, hkv),
+        *_prologue_args(prologue, batch * q_len, d),
         _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
     )
     return out
@@ -635,9 +715,14 @@ def verify_attention(
     if tokens % bs:
         raise ValueError(f"q holds {tokens} tokens, not a multiple of the {bs} requests")
     length = tokens // bs
+    if key_buffer.shape != value_buffer.shape or key_buffer.shape[2] != d:
+        raise ValueError(f"key_buffer and value_buffer must both be (pool, kv_heads, {d}); got "
+                         f"{tuple(key_buffer.shape)} and {tuple(value_buffer.shape)}")
     q = _bf16_rows(q, "q")
     k = _bf16_rows(k.view(-1, hkv, d), "k")
     v = _bf16_rows(v.view(-1, hkv, d), "v")
+    _need_rows(k, tokens, "k")
+    _need_rows(v, tokens, "v")
     key_buffer, value_buffer = _bf16_rows(key_buffer, "key_buffer"), _bf16_rows(value_buffer, "value_buffer")
     if out is None:
         out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
@@ -654,10 +739,12 @@ def verify_attention(
         mask = custom_mask.contiguous()
         if qlen_mask:
             mode = 2
+            _need_numel(mask, bs * length * length, "custom_mask")
         else:
             if mask_indptr is None:
                 raise ValueError("a custom mask in sglang's layout needs mask_indptr")
             mode, mptr = 1, _i64(mask_indptr)
+            _need_rows(mptr, bs, "mask_indptr")
     scale = d ** -0.5 if sm_scale is None else float(sm_scale)
     ctx = 0 if max_context is None else int(max_context)
     nbytes = verify_workspace_bytes(bs, length, hq, hkv, d, ctx, pool, q.device)
@@ -701,6 +788,10 @@ def block_self_attention(
     blocks, t, three, heads, d = qkv.shape
     if three != 3:
         raise ValueError(f"qkv must be (blocks, T, 3, heads, head_dim), got {tuple(qkv.shape)}")
+    rope.check(d)
+    _need_numel(q_norm, d, "q_norm")
+    _need_numel(k_norm, d, "k_norm")
+    _need_rows(positions, blocks * t, "positions")
     out = torch.empty((blocks, t, heads, d), dtype=torch.bfloat16, device=qkv.device)
     if blocks == 0:
         return out
@@ -742,6 +833,10 @@ def write_context_kv(
     hpc = heads_per_cache or heads
     if cache_ptrs.numel() * hpc < layers * heads:
         raise ValueError(f"{cache_ptrs.numel()} caches of {hpc} heads cannot hold {layers} x {heads} heads")
+    rope.check(d)
+    _need_numel(k_norm, layers * d, "k_norm")
+    _need_rows(positions, tokens, "positions")
+    _need_rows(slots, tokens, "slots")
     sb, sh, st, voff = cache_strides
     kn = _f32(k_norm)
     call(
@@ -778,6 +873,8 @@ def write_context_kv_pool(
     heads = kv_size // head_dim
     if kv.numel() != tokens * num_layers * 2 * kv_size:
         raise ValueError("kv must be (tokens, layers * 2 * kv_size)")
+    _check_pool_write(meta, k_norm_weights, rope, positions, locs, num_layers, head_dim, tokens, commit_lens,
+                      locs_row_width)
     cl = None if commit_lens is None else _i32(commit_lens)
     call(
         "fm_write_context_kv_pool",
@@ -785,6 +882,23 @@ def write_context_kv_pool(
         _f32(k_norm_weights).data_ptr(), *rope.args(), _i64(positions).data_ptr(), _i64(locs).data_ptr(),
         _ptr(cl), int(locs_row_width or 0), float(eps), _stream(kv),
     )
+
+
+def _check_pool_write(meta, k_norm_weights, rope, positions, locs, layers, head_dim, tokens, commit_lens,
+                      locs_row_width) -> None:
+    """Extents the pool writers read: meta rows per layer, weights, one position and
+    one location per token, one commit length per row of ``locs_row_width`` tokens."""
+    rope.check(head_dim)
+    if meta.dim() != 2 or meta.shape[1] != 4:
+        raise ValueError(f"meta must be (layers, 4), got {tuple(meta.shape)}")
+    _need_rows(meta, layers, "meta")
+    _need_numel(k_norm_weights, layers * head_dim, "k_norm_weights")
+    _need_numel(positions, tokens, "positions")
+    _need_numel(locs, tokens, "locs")
+    if commit_lens is not None:
+        if not locs_row_width:
+            raise ValueError("commit_lens needs locs_row_width")
+        _need_numel(commit_lens, -(-tokens // locs_row_width), "commit_lens")
 
 
 def _fp8_cache(t: torch.Tensor, name: str) -> None:
@@ -818,6 +932,10 @@ def write_context_kv_fp8(
     hpc = heads_per_cache or heads
     if cache_ptrs.numel() * hpc < layers * heads:
         raise ValueError(f"{cache_ptrs.numel()} caches of {hpc} heads cannot hold {layers} x {heads} heads")
+    rope.check(d)
+    _need_numel(k_norm, layers * d, "k_norm")
+    _need_rows(positions, tokens, "positions")
+    _need_rows(slots, tokens, "slots")
     if scales.numel() < 2 * layers:
         raise ValueError(f"scales must hold (layers, 2) = {2 * layers} values, got {scales.numel()}")
     sb, sh, st, voff = cache_strides
@@ -859,6 +977,8 @@ def write_context_kv_pool_fp8(
     heads = kv_size // head_dim
     if kv.numel() != tokens * num_layers * 2 * kv_size:
         raise ValueError("kv must be (tokens, layers * 2 * kv_size)")
+    _check_pool_write(meta, k_norm_weights, rope, positions, locs, num_layers, head_dim, tokens, commit_lens,
+                      locs_row_width)
     cl = None if commit_lens is None else _i32(commit_lens)
     call(
         "fm_write_context_kv_pool_fp8",
