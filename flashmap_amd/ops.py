@@ -200,7 +200,9 @@ def rms_norm_rope(
 
 class _WorkspacePool:
     """One persistent split-KV workspace per device, grown outside graph capture.
-    A replaced buffer is kept alive, since captured graphs may still point at it."""
+    A replaced buffer is kept alive, since captured graphs may still point at it.
+    Every call on the device uses it: calls on one stream are ordered, calls on two
+    streams that may overlap in time would race on it."""
 
     def __init__(self):
         self.buffers: dict[torch.device, torch.Tensor] = {}
