@@ -111,7 +111,8 @@ def test_fused_prologue_is_bit_identical(dev):
 # ----------------------------------------------------------------- paged (a6)
 
 
-@pytest.mark.parametrize("hq,hkv,page", [(32, 8, 16), (16, 16, 16), (40, 8, 16), (8, 2, 32), (8, 2, 8)])
+@pytest.mark.parametrize("hq,hkv,page", [(32, 8, 16), (16, 16, 16), (40, 8, 16), (8, 2, 32), (8, 2, 8), (8, 2, 64),
+                                          (8, 2, 128), (8, 2, 24), (8, 2, 1)])
 def test_paged_vllm_matches_oracle_and_contig(dev, hq, hkv, page):
     g = gen(6)
     d, t = 128, 16

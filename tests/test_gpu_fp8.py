@@ -91,7 +91,8 @@ def _e4m3(shape, g, scale=1.0):
 
 
 @pytest.mark.parametrize("page,d,hq,hkv", [(16, 128, 32, 8), (8, 64, 8, 2), (16, 128, 16, 16), (32, 64, 40, 8),
-                                         (16, 128, 48, 8), (8, 128, 24, 4)])
+                                         (16, 128, 48, 8), (8, 128, 24, 4), (64, 128, 8, 2), (128, 64, 16, 16),
+                                         (24, 128, 8, 2)])
 def test_paged_fp8_attention_descales(dev, page, d, hq, hkv):
     print(f"fp8 paged page={page} d={d} hq={hq} hkv={hkv}", flush=True)
     g = gen(60 + page + d + hq)
