@@ -171,6 +171,53 @@ def test_paged_large_batch(dev):
     check_close(got, want)
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 2)])
+def test_paged_ragged_query_rows(dev, hq, hkv):
+    """FlashAttention's varlen queries: requests with 16, 3, 0, 16, 9, 1 and 12 rows
+    (max_seqlen_q 16), contexts including an empty one; every row of ``cu_seqlens_q``'s
+    ranges against the oracle."""
+    g = gen(23)
+    d, page = 128, 16
+    rows = [16, 3, 0, 16, 9, 1, 12]
+    lens = torch.tensor([40, 700, 33, 0, 129, 16, 1])
+    b = len(rows)
+    cu = torch.zeros(b + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(rows), 0)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(int(cu[-1]), hq, d, generator=g).bfloat16()
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
+    want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
+    o = ops()
+    got = o.block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), 16,
+                                  lmax, d ** -0.5)
+    check_close(got, want)
+    assert (got[int(cu[3]):int(cu[4])] == 0).all()  # the empty context's 16 rows
+
+
+@pytest.mark.parametrize("t", [1, 5, 33, 48])
+def test_query_lengths_contig_and_token_paged(dev, t):
+    """Query blocks other than 16 rows (a head's rows spanning row blocks and units):
+    the contiguous and the token-paged layouts against the oracle and each other."""
+    g = gen(24 + t)
+    hq, hkv, d = 32, 8, 128
+    lens = torch.tensor([77, 1, 260])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    want = ref.block_attention_contig(q, k, v, lens)
+    o = ops()
+    got = o.block_attention_contig(q.to(dev), k.to(dev), v.to(dev), seqlens_k=lens.to(dev))
+    check_close(got, want)
+    kb, vb, pt = token_pool_from_contig(k, v, lens, g)
+    tok = o.block_attention_token_paged(q.to(dev), kb.to(dev), vb.to(dev), lens.to(dev, torch.int32), pt.to(dev))
+    assert torch.equal(tok, got), "token-paged and contiguous layouts must agree bit for bit"
+
+
 # ----------------------------------------------------------- token paged (a7)
 
 
