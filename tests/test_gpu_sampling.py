@@ -2,8 +2,8 @@
 the C ABI, against the CPU oracle (oracle/sampling.py):
 
 - argmax per row: exact (int64 indices) for bf16 / fp16 / fp32 logits, ties to the first
-  index, all -inf rows, NaN rows, strided rows, vocabularies that end mid-chunk, a
-  151936-entry vocabulary;
+  index, all -inf rows, NaN rows, strided rows, vocabularies that end mid-chunk or on a
+  whole number of tiles, a 151936-entry vocabulary;
 - the fused sampler: greedy rows exact; sampled rows equal the oracle's tokens wherever
   the oracle's winning key beats the runner-up by more than 1e-4 (the random words are
   exact, the logs may differ in the last ulp); int32 offset wraparound past 2^31;
@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("rows,vocab,stride", [(1, 1, 1), (3, 100, 100), (17, 8193, 8200), (5, 24581, 24581),
-                                               (64, 151936, 151936)])
+                                               (3, 32768, 32768), (64, 151936, 151936)])
 def test_argmax_rows(dev, dtype, rows, vocab, stride):
     g = gen(rows + vocab)
     x = torch.randn(rows, stride, generator=g).to(dtype)[:, :vocab]
