@@ -1,0 +1,128 @@
+"""The benchmark configurations, each run as its own call on the GPU and checked against
+the float32 oracle (max-abs 2e-2, mean-abs 2e-3 on the bf16 outputs):
+
+- C1's shape: hidden 1024, 16 q / 8 KV heads, head_dim 64, K = 16 draft rows, batch 1,
+  512 context positions, drawn as the configuration states it (hidden states N(0, 1),
+  projection weights N(0, 0.02), QK-RMSNorm weight 1, eps 1e-6, RoPE theta 1e6, query
+  positions 512 + 0..15); keys k-normed and rotated by the GPU prologue, the queries'
+  prologue fused into the contiguous attention call;
+- C2 at its full size: contiguous batch 1 x 2048 positions, 32 q / 8 KV heads, head_dim
+  128, fused prologue, query positions 2048 + 0..15;
+- C3 (batch 64, contexts U[256, 8192]), C4 (batch 8 x 32768) and C5 (GQA 5, batch 32,
+  U[1024, 8192]): exactly the call bench.py times -- the query prologue fused, the step
+  plan computed once and passed in, the paged op over the cache the context writer
+  filled -- with every sequence of the batch checked against the oracle's prologue,
+  block-table gather and attention.
+"""
+
+import pytest
+import torch
+
+from _inputs import check_close
+from oracle import attention as ref
+
+pytestmark = pytest.mark.gpu
+
+EPS, THETA = 1e-6, 1e6
+
+
+def _ops():
+    from flashmap_amd import ops
+
+    return ops
+
+
+def test_c1_shape_fused_prologue(dev):
+    ops = _ops()
+    hidden, hq, hkv, d, k_rows, ctx = 1024, 16, 8, 64, 16, 512
+    print("C1 shape: hidden 1024, 16/8 heads, D 64, ctx 512", flush=True)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, k_rows, hidden, generator=g)
+    h = torch.randn(1, ctx, hidden, generator=g)
+    wq = torch.randn(hq * d, hidden, generator=g) * 0.02
+    wk = torch.randn(hkv * d, hidden, generator=g) * 0.02
+    wv = torch.randn(hkv * d, hidden, generator=g) * 0.02
+    q_pre = (x @ wq.T).bfloat16().view(1, k_rows, hq, d)
+    k_pre = (h @ wk.T).bfloat16().view(ctx, hkv, d)
+    v = (h @ wv.T).bfloat16().view(1, ctx, hkv, d).transpose(1, 2).contiguous()
+    w = torch.ones(d)
+    table = ref.rope_table(ctx + k_rows + 1, d, THETA)
+    kpos, qpos = torch.arange(ctx), ctx + torch.arange(k_rows)
+
+    rope = ops.rope_from_table(table.to(dev))
+    keys = ops.rms_norm_rope(k_pre.to(dev), w.to(dev), rope, kpos.to(dev), EPS)
+    want_keys = ref.rms_norm_rope_vllm(k_pre, w, table, kpos, EPS)
+    assert (keys.cpu() == want_keys).float().mean() > 0.99
+    keys = keys.view(1, ctx, hkv, d).transpose(1, 2).contiguous()
+    got = ops.block_attention_contig(q_pre.to(dev), keys, v.to(dev), d ** -0.5,
+                                     prologue=ops.Prologue(w.to(dev), rope, qpos.to(dev), EPS))
+    qn = ref.rms_norm_rope_vllm(q_pre.view(k_rows, hq, d), w, table, qpos, EPS).view(1, k_rows, hq, d)
+    want = ref.block_attention_contig(qn, want_keys.view(1, ctx, hkv, d).transpose(1, 2), v)
+    err = check_close(got, want)
+    print(f"C1: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+
+
+def test_c2_full_size_fused_prologue(dev):
+    ops = _ops()
+    hq, hkv, d, k_rows, ctx = 32, 8, 128, 16, 2048
+    print("C2 full size: contiguous 1 x 2048, 32/8 heads, D 128", flush=True)
+    g = torch.Generator().manual_seed(0)
+    q_pre = torch.randn(1, k_rows, hq, d, generator=g).bfloat16()
+    keys = torch.randn(1, hkv, ctx, d, generator=g).bfloat16()
+    values = torch.randn(1, hkv, ctx, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(ctx + k_rows + 1, d, THETA)
+    qpos = ctx + torch.arange(k_rows)
+    pro = ops.Prologue(w.to(dev), ops.rope_from_table(table.to(dev)), qpos.to(dev), EPS)
+    got = ops.block_attention_contig(q_pre.to(dev), keys.to(dev), values.to(dev), d ** -0.5, prologue=pro)
+    qn = ref.rms_norm_rope_vllm(q_pre.view(k_rows, hq, d), w, table, qpos, EPS).view(1, k_rows, hq, d)
+    want = ref.block_attention_contig(qn, keys, values)
+    err = check_close(got, want)
+    print(f"C2: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+
+
+def _bench_call(dev, workload):
+    """The inputs and the output of bench.py's timed call for ``workload``."""
+    import bench
+
+    ops = _ops()
+    inp = bench.build_inputs(workload)
+    batch, hkv, d, k_rows, page = (inp[k] for k in ("batch", "hkv", "d", "k_rows", "page"))
+    table = ref.rope_table(inp["hi"] + k_rows + 1, d, THETA)
+    rope = ops.rope_from_table(table.to(dev))
+    w = torch.ones(d, device=dev)
+    lens = inp["lens"].to(dev, torch.int32)
+    cache = torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.bfloat16, device=dev)
+    ptrs = torch.tensor([cache.data_ptr()], dtype=torch.int64, device=dev)
+    ops.write_context_kv(inp["kv_pre"].to(dev), inp["positions"].to(dev), inp["slots"].to(dev),
+                         w[None].expand(1, d).contiguous(), rope, ptrs,
+                         (cache.stride(0), cache.stride(1), cache.stride(2), d), page, EPS)
+    qpos = torch.cat([int(n) + torch.arange(k_rows) for n in inp["lens"]])
+    cu = (torch.arange(batch + 1, dtype=torch.int32) * k_rows).to(dev)
+    pro = ops.Prologue(w, rope, qpos.to(dev), EPS)
+    plan = ops.attention_plan(lens)
+    out = ops.block_attention_paged(inp["q_pre"].to(dev), cache, cu, lens, inp["bt"].to(dev), k_rows, inp["hi"],
+                                    d ** -0.5, prologue=pro, plan=plan)
+    torch.cuda.synchronize()
+    return inp, table, qpos, cache, out
+
+
+@pytest.mark.parametrize("workload", ["c3-qwen3-8b-paged-b64", "c4-qwen3-8b-long-b8", "c5-27b-gqa5-b32"])
+def test_bench_call_every_sequence(dev, workload):
+    print(f"bench call {workload}", flush=True)
+    inp, table, qpos, cache, out = _bench_call(dev, workload)
+    k_rows, d, hq = inp["k_rows"], inp["d"], inp["hq"]
+    w = torch.ones(d)
+    qn = ref.rms_norm_rope_vllm(inp["q_pre"], w, table, qpos, EPS)
+    bt = inp["bt"]
+    worst = 0.0
+    for b in range(inp["batch"]):
+        n = int(inp["lens"][b])
+        pages = bt[b, :(n + inp["page"] - 1) // inp["page"]].long().to(dev)
+        rows = cache[pages].transpose(1, 2).reshape(-1, inp["hkv"], 2 * d)[:n].float().cpu()  # (n, Hkv, 2D)
+        k, v = rows[..., :d].transpose(0, 1), rows[..., d:].transpose(0, 1)
+        want = ref.attention(qn[b * k_rows:(b + 1) * k_rows].float().transpose(0, 1), k, v, d ** -0.5)
+        err = check_close(out[b * k_rows:(b + 1) * k_rows].cpu().float(), want.transpose(0, 1))
+        worst = max(worst, err.max().item())
+    assert out.shape == (inp["batch"] * k_rows, hq, d)
+    print(f"{workload}: {inp['batch']} sequences, worst max-abs {worst:.3e}", flush=True)
