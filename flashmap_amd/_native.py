@@ -48,6 +48,12 @@ SIGNATURES: dict[str, tuple] = {
         [*_Q, P, I64, I64, I64, I64, I64, I32, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,
          *_PROLOGUE, *_SPLIT],
     ),
+    "fm_static_scratch_bytes": (c_size_t, []),
+    "fm_block_attn_paged_static": (
+        c_int,
+        [*_Q, P, I64, I64, I64, I64, I64, I32, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,
+         *_PROLOGUE, P, P],
+    ),
     "fm_block_attn_paged_runs": (
         c_int,
         [*_Q, P, P, P, I32, I32, I64, I64, I64, I64, I64, I32, P, I64, I64, P, I32, I32, I32, I32, I32, I32,

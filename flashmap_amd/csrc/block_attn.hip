@@ -1605,6 +1605,7 @@ struct CommonIn {
   void *ws;
   size_t ws_bytes;
   hipStream_t stream;
+  bool static_ws = false;  // ws is the library's static scratch (fm_block_attn_paged_static)
 };
 
 // vf: a verify call (its combine also attends to the verify tokens).
@@ -1650,6 +1651,11 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   Sizing sz;
   int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, a.f8 != 0);
   if (rc != FM_OK) return rc;
+  if (c.static_ws && sz.bytes > c.ws_bytes)
+    return fail(FM_ERR_WORKSPACE,
+                "this call needs %zu bytes of scratch; the library's static scratch holds %zu bytes "
+                "(use fm_block_attn_paged with a workspace of fm_attn_workspace_bytes)",
+                sz.bytes, c.ws_bytes);
   if (c.ws == nullptr || c.ws_bytes < sz.bytes)
     return fail(FM_ERR_WORKSPACE, "workspace of %zu bytes, need %zu", c.ws_bytes, sz.bytes);
   FM_REQUIRE(al16(c.ws), "workspace must be 16-byte aligned");
@@ -1860,6 +1866,61 @@ extern "C" int fm_block_attn_paged(
   int layout = 0;
   const int rc = setup_paged(a, layout, kv_cache, num_blocks, stride_block, stride_head, stride_token, v_offset,
                              page_size, block_table, block_table_stride, block_table_width, seqused_k, 2);
+  return rc != FM_OK ? rc : run_attention(c, layout, a);
+}
+
+// The workspace of fm_block_attn_paged_static: device memory the library holds itself
+// (one copy per GPU the library runs on, kept until the process ends) for callers that
+// cannot allocate. Host code never passes `scratch` itself to a kernel (in host code the
+// name is a host-side stand-in): it takes the array's device address per device with
+// hipGetSymbolAddress once, with that device current, and uses that address.
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[STATIC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static std::vector<void *> g_scratch_ptr;  // per device: the address of its `scratch`
+
+static int static_scratch(void **ptr) {
+  int dev = 0;
+  FM_CHECK_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(FM_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return FM_OK;
+}
+
+extern "C" size_t fm_static_scratch_bytes(void) { return STATIC_SCRATCH_BYTES; }
+
+extern "C" int fm_block_attn_paged_static(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head, void *out,
+    int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *kv_cache, int64_t num_blocks, int64_t stride_block,
+    int64_t stride_head, int64_t stride_token, int64_t v_offset, int32_t page_size,
+    const int32_t *block_table, int64_t block_table_stride, int64_t block_table_width,
+    const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+    const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *stream) {
+  void *ws = nullptr;
+  int rc = static_scratch(&ws);
+  if (rc != FM_OK) return rc;
+  CommonIn c{q, q_stride_batch, q_stride_token, q_stride_head, out, out_stride_batch,
+             out_stride_token, out_stride_head, cu_seqlens_q, batch, max_seqlen_q, max_seqlen_k,
+             num_q_heads, num_kv_heads, head_dim, softmax_scale, q_norm_weight, rope_cos,
+             rope_sin, rope_row_stride, rope_pair_stride, rope_rows, q_positions, eps, plan,
+             ws, STATIC_SCRATCH_BYTES, (hipStream_t)stream, true};
+  AttnArgs a{};
+  int layout = 0;
+  rc = setup_paged(a, layout, kv_cache, num_blocks, stride_block, stride_head, stride_token, v_offset,
+                   page_size, block_table, block_table_stride, block_table_width, seqused_k, 2);
   return rc != FM_OK ? rc : run_attention(c, layout, a);
 }
 

@@ -376,6 +376,54 @@ def block_attention_paged(
     ``cu_seqlens_q``) onto vLLM's paged cache ``(num_blocks, Hkv, page, 2D)`` (K then V
     in every token row), each request reading its first ``seqused_k[b]`` positions
     through ``block_table`` (flashmap/vllm/model.py:93-134)."""
+    prep = _paged_call(query, kv_cache, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k,
+                       softmax_scale, prologue, plan, out)
+    if prep.args is None:
+        return prep.out
+    ws = workspace_for(prep.batch, max_seqlen_q, prep.hq, prep.hkv, prep.d, max_seqlen_k, query.device)
+    call("fm_block_attn_paged", *prep.args, ws.data_ptr(), ws.numel(), _stream(query))
+    return prep.out
+
+
+def block_attention_paged_static(
+    query: torch.Tensor,
+    kv_cache: torch.Tensor,
+    cu_seqlens_q: torch.Tensor | None,
+    seqused_k: torch.Tensor,
+    block_table: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    prologue: Prologue | None = None,
+    plan: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`block_attention_paged` through ``fm_block_attn_paged_static``: no workspace,
+    the library's per-GPU static scratch instead (for callers that cannot allocate
+    device memory). Pass ``out`` to allocate nothing at all. Calls that may overlap in
+    time on one GPU race on the scratch; a call needing more than
+    ``fm_static_scratch_bytes()`` raises."""
+    prep = _paged_call(query, kv_cache, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k,
+                       softmax_scale, prologue, plan, out)
+    if prep.args is not None:
+        call("fm_block_attn_paged_static", *prep.args, _stream(query))
+    return prep.out
+
+
+@dataclass
+class _PagedCall:
+    out: torch.Tensor
+    args: list | None  # None: nothing to launch
+    batch: int = 0
+    hq: int = 0
+    hkv: int = 0
+    d: int = 0
+
+
+def _paged_call(query, kv_cache, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k, softmax_scale,
+                prologue, plan, out) -> _PagedCall:
+    """Checks of a vLLM-layout call and its C arguments up to the plan (the entry points
+    differ only in what follows: a workspace, or none)."""
     _check_cuda(query, kv_cache, cu_seqlens_q, seqused_k, block_table)
     if kv_cache.dtype != torch.bfloat16:
         raise TypeError(f"kv_cache must be bfloat16, got {kv_cache.dtype}")
@@ -389,23 +437,24 @@ def block_attention_paged(
     _check_requests(batch, cu_seqlens_q, tokens, max_seqlen_q, block_table, "block_table", plan)
     query, out, qs, os_ = _q_out(query, out, varlen=True)
     if batch == 0 or tokens == 0:
-        return out
+        return _PagedCall(out, None)
     cu = None if cu_seqlens_q is None else _i32(cu_seqlens_q)
     if cu is None:
         qs[0], os_[0] = max_seqlen_q * qs[1], max_seqlen_q * os_[1]
     bt = block_table if (block_table.dtype == torch.int32 and block_table.stride(-1) == 1) else _i32(block_table)
     sk = _i32(seqused_k)
-    ws = workspace_for(batch, max_seqlen_q, hq, hkv, d, max_seqlen_k, query.device)
-    call(
-        "fm_block_attn_paged",
+    args = [
         query.data_ptr(), *qs, out.data_ptr(), *os_, _ptr(cu),
         kv_cache.data_ptr(), num_blocks, kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), d, page,
         bt.data_ptr(), bt.stride(0), bt.shape[1], sk.data_ptr(), batch, max_seqlen_q, max_seqlen_k,
         hq, hkv, d, float(softmax_scale),
         *_prologue_args(prologue, tokens, d),
-        _ptr(plan), ws.data_ptr(), ws.numel(), _stream(query),
-    )
-    return out
+        _ptr(plan),
+    ]
+    # Tensors converted above (int32 copies, contiguous rows) must outlive the launch.
+    prep = _PagedCall(out, args, batch, hq, hkv, d)
+    prep.keep = (query, cu, bt, sk)
+    return prep
 
 
 def block_attention_paged_runs(

@@ -147,6 +147,28 @@ int fm_block_attn_paged(
     const int64_t *q_positions, float eps, const int32_t *plan, void *workspace,
     size_t workspace_bytes, void *stream);
 
+/* fm_block_attn_paged for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). It has no
+ * counterpart in the reference. It takes fm_block_attn_paged's arguments without the
+ * workspace and uses instead a scratch array the library holds in device memory
+ * (fm_static_scratch_bytes() = 32 MiB per GPU it runs on, kept until the process ends);
+ * it allocates nothing and never synchronizes. A call whose split-KV scratch would exceed
+ * the array fails with FM_ERR_WORKSPACE. Every call on one GPU shares that GPU's array:
+ * calls that may overlap in time on one GPU (two streams, two threads) race on it. No
+ * part of the array has to start cleared (each call writes what it later reads). */
+size_t fm_static_scratch_bytes(void);
+int fm_block_attn_paged_static(
+    const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
+    void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
+    const int32_t *cu_seqlens_q, const void *kv_cache, int64_t num_blocks, int64_t stride_block,
+    int64_t stride_head, int64_t stride_token, int64_t v_offset, int32_t page_size,
+    const int32_t *block_table, int64_t block_table_stride, int64_t block_table_width,
+    const int32_t *seqused_k, int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+    const float *q_norm_weight, const float *rope_cos, const float *rope_sin,
+    int64_t rope_row_stride, int64_t rope_pair_stride, int64_t rope_rows,
+    const int64_t *q_positions, float eps, const int32_t *plan, void *stream);
+
 /* f4: one drafter layer's paged attention over vLLM's virtual context-cache layout
  * (flashmap/vllm/context_cache.py:33-73), where the layer's KV heads lie in runs across
  * several caches of one geometry and one block table: run r holds the next run_count[r]
