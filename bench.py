@@ -12,6 +12,11 @@ the step's plan (computed once per step and shared by every layer, like
 FlashAttention's scheduler metadata) prepared before the timed region. Inputs are
 resident in HBM when timing starts.
 
+Timing: W warm-up calls and K timed calls right after set-up are reported as
+`cold_us_per_call`; then the call runs back to back for `--settle-ms` while the GPU's
+power controller settles (a load this heavy starting from idle first has its clocks cut
+for some milliseconds), then W warm-up calls and exactly K timed calls give `value`.
+
 Prints one JSON line. `value` is microseconds per call (lower is better); the line
 also carries the achieved HBM bandwidth, a roofline record for the main attention
 kernel (algorithmic bytes / its average duration from HIP events recorded around
@@ -76,6 +81,22 @@ def build_inputs(name: str, seed: int = 0):
                        for b, n in enumerate(lens)])
     return dict(batch=batch, hq=hq, hkv=hkv, d=d, k_rows=k_rows, page=page, lens=lens, bt=bt, total=total,
                 q_pre=q_pre, kv_pre=kv_pre, positions=positions, slots=slots, lo=lo, hi=hi)
+
+
+def mfma_record(workload: str, flops: float, kernel_ms: float, fp8: bool) -> dict:
+    """MFMA utilisation of the main kernel: from the rocprofv3 counters committed under
+    profiles/ for this workload (SQ_VALU_MFMA_BUSY_CYCLES over the SIMD-cycles of the
+    dispatch), beside the algorithmic FLOPs over the HIP-event duration."""
+    rec = {"tflops_algorithmic": round(flops / (kernel_ms * 1e-3) / 1e12, 1),
+           "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+           "util_algorithmic": round(flops / (kernel_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    name = "attn_fwd_" + workload.split("-", 1)[0] + "_paged_b64" + ("_fp8" if fp8 else "") + ".mfma.json"
+    f = ROOT / "profiles" / name
+    if f.exists():
+        c = json.loads(f.read_text())
+        if c.get("workload") == workload:
+            rec.update({"util": c["util"], "source": f"profiles/{name}", "counters": c["counters"]})
+    return rec
 
 
 def algorithmic_bytes(inp, kv_bytes: int = 2) -> dict:
@@ -213,16 +234,8 @@ def run_select(args, dev) -> dict:
     else:
         def call():
             ops.sample_rows(logits, temps, greedy, seed)
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        call()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    timing = _measure(call, args, kernel_events=False)
+    ms = timing["ms"]
     total = rows * vocab * 2 + rows * 8
     gbs = total / (ms * 1e-3) / 1e9
     result = {
@@ -236,6 +249,7 @@ def run_select(args, dev) -> dict:
                      "note": "whole call (tile pass + row pass) from events around the calls"
                              + ("; the sampled path is ALU-bound: one Philox-4x32-10 and two logs per logit"
                                 if mode == "sample" else "")},
+        **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
         from oracle import sampling as S
@@ -283,7 +297,7 @@ def run_contig(args, dev) -> dict:
     def call():
         ops.block_attention_contig(qd, kd, vd, d ** -0.5, prologue=pro, out=out)
 
-    ms, kernel_ms = _time_call(call, args)
+    ms, kernel_ms, timing = _time_call(call, args)
     kv = batch * hkv * ctx * d * 2 * 2
     total = kv + 2 * batch * k_rows * hq * d * 2 + batch * k_rows * d * 4
     gbs = total / (kernel_ms * 1e-3) / 1e9
@@ -298,6 +312,7 @@ def run_contig(args, dev) -> dict:
         "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": total,
                      "kernel_us": round(kernel_ms * 1e3, 2)},
+        **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
@@ -312,31 +327,76 @@ def run_contig(args, dev) -> dict:
     return result
 
 
-def _time_call(call, args) -> tuple[float, float]:
-    """(ms per call, ms per main-kernel launch from the library's HIP events)."""
+def _events_ms(call, steps: int) -> float:
+    """ms per call over exactly ``steps`` back-to-back calls, bracketed by synchronizations."""
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _measure(call, args, kernel_events: bool = True) -> dict:
+    """The timing protocol of every workload.
+
+    1. cold: W warm-up calls, then K timed calls, right after the set-up (the GPU has
+       been idle): reported, not the value.
+    2. settle: back-to-back calls for ``--settle-ms`` (default 100 ms). When a load this
+       heavy starts, the GPU's power controller first cuts the clocks (measured: the main
+       kernel goes from 165 us to about 205 us within 4 ms of the load's start and comes
+       back over about 25 ms; a plain 1 GiB copy shows no such dip), so calls timed inside
+       that window measure the controller's transient, not the sustained rate.
+    3. the value: W warm-up calls, then exactly K timed calls.
+    4. the main kernel alone: K calls with HIP events recorded around each of its
+       launches on its stream (fm_profile_*).
+    """
     import ctypes
 
     from flashmap_amd import _native
 
     for _ in range(args.warmup):
         call()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
+    cold = _events_ms(call, args.steps)
+    settle_calls = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < args.settle_ms:
+        for _ in range(10):
+            call()
+        settle_calls += 10
+        torch.cuda.synchronize()
+    settle_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(args.warmup):
         call()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    lib = _native.lib()
-    lib.fm_profile_enable(1)
-    for _ in range(args.steps):
-        call()
-    torch.cuda.synchronize()
-    tot, cnt = ctypes.c_double(), ctypes.c_int64()
-    _native.call("fm_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
-    lib.fm_profile_enable(0)
-    return ms, tot.value / max(cnt.value, 1)
+    ms = _events_ms(call, args.steps)
+    kernel_ms = None
+    if kernel_events:
+        lib = _native.lib()
+        lib.fm_profile_enable(1)
+        for _ in range(args.steps):
+            call()
+        torch.cuda.synchronize()
+        tot, cnt = ctypes.c_double(), ctypes.c_int64()
+        _native.call("fm_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
+        lib.fm_profile_enable(0)
+        kernel_ms = tot.value / max(cnt.value, 1)
+    return {"ms": ms, "kernel_ms": kernel_ms, "cold_ms": cold,
+            "settle": {"ms": round(settle_ms, 1), "calls": settle_calls}}
+
+
+def _timing_fields(t: dict) -> dict:
+    """The extra keys every bench line carries about its timing protocol."""
+    return {"cold_us_per_call": round(t["cold_ms"] * 1e3, 2), "settle": t["settle"],
+            "timing": "value: K back-to-back calls after --settle-ms of calls and W warm-ups; "
+                      "cold_us_per_call: the same K calls before the settling, right after set-up"}
+
+
+def _time_call(call, args) -> tuple[float, float, dict]:
+    """(ms per call, ms per main-kernel launch, the timing record)."""
+    t = _measure(call, args)
+    return t["ms"], t["kernel_ms"], t
 
 
 def run_tree(args, dev) -> dict:
@@ -366,7 +426,7 @@ def run_tree(args, dev) -> dict:
     def call():
         ops.block_attention_token_paged(q, kb, vb, lens_d, pt_d, plan=plan, out=out)
 
-    ms, kernel_ms = _time_call(call, args)
+    ms, kernel_ms, timing = _time_call(call, args)
     kv = ctx * hkv * d * 2 * 2
     total = kv + 4 * ctx + 4 * requests + 2 * requests * q_len * hq * d * 2
     flops = 4 * q_len * hq * d * ctx
@@ -390,6 +450,7 @@ def run_tree(args, dev) -> dict:
     }
     result["roofline"].update({"kernel": "attn_fwd_kernel", "traffic": None, "bytes_per_launch": total,
                                "flops_per_launch": flops, "kernel_us": round(kernel_ms * 1e3, 2)})
+    result.update(_timing_fields(timing))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = tree_cpu_baseline(q, kb, vb, lens, pt, args.cpu_budget)
     return result
@@ -453,25 +514,7 @@ def run_verify(args, dev) -> dict:
         ops.verify_attention(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, None, mask == "qlen", out=out,
                              max_context=hi)
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        call()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    lib = _native.lib()
-    lib.fm_profile_enable(1)
-    for _ in range(args.steps):
-        call()
-    torch.cuda.synchronize()
-    tot, cnt = ctypes.c_double(), ctypes.c_int64()
-    _native.call("fm_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
-    lib.fm_profile_enable(0)
-    kernel_ms = tot.value / max(cnt.value, 1)
+    ms, kernel_ms, timing = _time_call(call, args)
     kv = ctx * hkv * d * 2 * 2
     total = kv + 4 * ctx + 4 * (batch + 1) + 2 * batch * length * hq * d * 2 + batch * length * hkv * d * 2 * 2
     achieved = total / (kernel_ms * 1e-3) / 1e9
@@ -493,6 +536,7 @@ def run_verify(args, dev) -> dict:
         "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "bytes_per_launch": total, "kernel_us": round(kernel_ms * 1e3, 2)},
+        **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = verify_cpu_baseline(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, mask, lens,
@@ -540,6 +584,8 @@ def main() -> int:
                     + sorted(CONTIG_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="back-to-back calls before the timed ones (the GPU's clocks settle under the load)")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="only run N copies of a 1 GiB buffer (HBM counter calibration)")
     args = ap.parse_args()
@@ -625,29 +671,7 @@ def main() -> int:
             ops.block_attention_paged(q_pre, cache, cu, lens, bt, k_rows, max_k, d ** -0.5,
                                       prologue=pro, plan=plan, out=out)
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(args.steps):
-        call()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-
-    # The main kernel alone: HIP events around each launch on its stream.
-    lib = _native.lib()
-    lib.fm_profile_enable(1)
-    for _ in range(args.steps):
-        call()
-    torch.cuda.synchronize()
-    import ctypes
-
-    tot, cnt = ctypes.c_double(), ctypes.c_int64()
-    _native.call("fm_profile_read", ctypes.byref(tot), ctypes.byref(cnt))
-    lib.fm_profile_enable(0)
-    kernel_ms = tot.value / max(cnt.value, 1)
+    ms, kernel_ms, timing = _time_call(call, args)
 
     ab = algorithmic_bytes(inp, kv_bytes=1 if fp8 else 2)
     traffic = None
@@ -678,7 +702,7 @@ def main() -> int:
             "ctx_lo": inp["lo"], "ctx_hi": inp["hi"], "ctx_sum": ab["sum_l"], "page": page,
             "layout": "vllm paged (blocks, kv_heads, page, 2*head_dim)" + (
                 f", virtual context-cache layout: caches of {virtual[1]} heads, runs {runs}" if virtual else ""),
-            "prologue": "fused",
+            "prologue": "QK-RMSNorm + RoPE applied by the call's query pass (its own launch)",
             "kv_dtype": "e4m3" if fp8 else "bf16",
         },
         "hbm_tbs": round(ab["total"] / (ms * 1e-3) / 1e12, 3),
@@ -694,11 +718,8 @@ def main() -> int:
             "bytes_per_launch": ab["total"],
             "kernel_us": round(kernel_ms * 1e3, 2),
         },
-        "mfma": {
-            "tflops": round(ab["flops"] / (kernel_ms * 1e-3) / 1e12, 1),
-            "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
-            "util": round(ab["flops"] / (kernel_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        },
+        "mfma": mfma_record(args.workload, ab["flops"], kernel_ms, fp8),
+        **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(inp, args.cpu_budget)
