@@ -1026,7 +1026,10 @@ __device__ __forceinline__ void out_write(char *slot, const u32x2_t (&h)[D / 16]
   using O = OutSlot<D, W>;
   typedef __attribute__((address_space(3))) u32x2_t lds_u32x2_t;
   typedef __attribute__((address_space(3))) f32x2_t lds_f32x2_t;
-  const int r = wave * 16 + n;
+  int r = wave * 16 + n;
+  // Opaque to the optimizer: the addresses below are formed here, once per partial,
+  // instead of being hoisted out of the tile loop and held in registers throughout it.
+  asm volatile("" : "+v"(r));
 #pragma unroll
   for (int db = 0; db < D / 16; ++db) {
     const int c = 2 * db + (g >> 1);
@@ -1108,6 +1111,207 @@ __device__ __forceinline__ void held_store(const AttnArgs &a, const HeldPartial<
 // LDS writes of this wavefront complete (before a barrier that publishes them).
 __device__ __forceinline__ void lds_publish() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// ---------------------------------------------------------------------------------
+// Direct query rows (bf16 calls without verify tokens, q_len <= QTOK): the consumers read
+// their rows straight from the caller's layout and apply the QK-RMSNorm + RoPE prologue
+// themselves at each segment's start, with norm_rope_apply, the code the standalone
+// prologue runs (the values are bit-identical to it). What the prologue reads is staged
+// in LDS, so that no global load waits on the tile path:
+//   - at kernel start, per sequence: its first query token row and draft rows, and the
+//     rotary table row of each of its first QTOK draft tokens (positions resolved and
+//     clamped), plus the norm weights;
+//   - per unit, the rotary records (D floats: the table row's cos / sin of every pair) of
+//     the QTOK tokens, brought into the replica's rope buffer by LDS-DMA that the consumer
+//     wavefronts issue at the second tile of the previous unit's segment and await (their
+//     own vmcnt) at its last tile, before the barrier that opens the unit;
+//   - the next unit's raw rows, loaded into registers a unit ahead (as the packed rows
+//     of the other calls are).
+// A unit whose records are not in the buffer (the share's first, one after a segment of a
+// single tile, or after sequences without context) reads its operands with global loads.
+// The prologue runs inside the workgroup's barrier cycle (about 1.5 us per segment start
+// at 64 rows x D 128, against a 1.25 us tile), so direct rows pay per segment what the
+// query pass pays once per call: the host takes them for small calls only (one unit per
+// two shares or fewer), where every share starts about one segment and a launch is saved.
+constexpr int QTOK = 16;
+
+template <int D, int W, bool F8, bool DQ>
+__host__ __device__ constexpr int kernel_seq_cap() {
+  using G = Geo<D, F8>;
+  constexpr int fixed = replicas(W) * (G::SMEM + OutSlot<D, W>::BYTES) + (DQ ? replicas(W) * QTOK * D * 4 + D * 4 : 0);
+  constexpr int per = 8 + (DQ ? 8 + 4 * QTOK : 0);  // (prefix, length); (first token, rows) and rope rows
+  constexpr int cap = (163840 - fixed - 1024) / per - 1;
+  return cap < SEQ_LDS ? cap : SEQ_LDS;
+}
+
+// Row of this lane in unit u for a direct call: draft row or not, its token within the
+// sequence, and the element offset of its channel 8 g in the caller's query.
+struct QRowD {
+  bool ok;
+  int tq;
+  int64_t off;
+};
+__device__ __forceinline__ QRowD direct_row(const AttnArgs &a, lds_i32x2_t *qmeta, int u, int r, int g) {
+  asm volatile("" : "+v"(r), "+v"(g));  // formed per call, not held across the tile loop
+  const int b = u / a.ups, ul = u - b * a.ups;
+  const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
+  const i32x2_t e = qmeta[b];  // (first token, rows)
+  const int R = rg * 16 * a.nrb + r;
+  const int gq = R / a.q_len, tq = R - gq * a.q_len;
+  QRowD x;
+  x.ok = gq < a.group && tq < e[1];
+  x.tq = x.ok ? tq : 0;
+  const int64_t tok = (int64_t)e[0] + x.tq;
+  const int64_t head = (int64_t)h * a.group + (x.ok ? gq : 0);
+  x.off = (a.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)x.tq * a.q_st) + head * a.q_sh + 8 * g;
+  return x;
+}
+
+// The token (record index, < q_len) of this lane's row r in unit u. A row past its
+// sequence's draft rows names some token too; its values are zeroed after the prologue.
+__device__ __forceinline__ int direct_tq(const AttnArgs &a, int u, int r) {
+  const int ul = u - (u / a.ups) * a.ups;
+  const int R = (ul - (ul / a.rgroups) * a.rgroups) * 16 * a.nrb + r;
+  return R - (R / a.q_len) * a.q_len;
+}
+
+__device__ __forceinline__ void direct_load_rows(const AttnArgs &a, const QRowD &x, u32x4_t (&q)[4]) {
+  typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
+  const uint16_t *src = a.q + x.off;
+  if (x.ok) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) q[t] = *(g_u32x4_t *)(src + 32 * t);
+  }
+}
+__device__ __forceinline__ void direct_load_rows(const AttnArgs &a, const QRowD &x, u32x4_t (&q)[2]) {
+  typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
+  const uint16_t *src = a.q + x.off;
+  if (x.ok) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) q[t] = *(g_u32x4_t *)(src + 32 * t);
+  }
+}
+
+// The rope buffer's record of token t (D floats): the table row as it lies (interleaved
+// (cos, sin) pairs), or cos of the D/2 pairs then their sin (split tables). LDS-DMA of the
+// QTOK records of sequence b: 16-byte chunk k of the records (k = 64 m + lane) is issued
+// by wavefront m % W, so every consumer wavefront issues ceil(NCH / W) of them.
+typedef __attribute__((address_space(3))) const int32_t lds_i32_t;
+
+template <int D, int W>
+__device__ __forceinline__ void rope_records_dma(const AttnArgs &a, lds_i32_t *rrow_b, char *rbuf, int wave,
+                                                 int lane) {
+  constexpr int CPT = D * 4 / 16;               // chunks per record
+  constexpr int NI = QTOK * CPT / 64;           // 1 KB DMA instructions per unit
+  constexpr int PER = (NI + W - 1) / W;         // per consumer wavefront
+  const bool il = a.rope.pair_stride == 2;
+  asm volatile("" : "+v"(lane));  // per-lane offsets formed here, not held across the tile loop
+  // Every table row first: an LDS read after an LDS-DMA would wait for the DMA's writes.
+  const float *src[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int m = wave + p * W;
+    const int k = 64 * (m < NI ? m : 0) + lane, t = k / CPT, j = k - (k / CPT) * CPT;
+    const int64_t rr = rrow_b[t];
+    src[p] = il || j < CPT / 2 ? a.rope.cos + rr * a.rope.row_stride + 4 * j
+                               : a.rope.sin + rr * a.rope.row_stride + 4 * (j - CPT / 2);
+  }
+  // Issued as inline asm, outside the compiler's LDS-DMA tracking: through the builtin, the
+  // compiler would make every later LDS access of this wavefront (the tile's K reads, the
+  // partial's hand-off) wait for these loads, which queue behind the producer's stream.
+  // The callers await them explicitly (wait_vm<0> before the barrier that publishes them).
+  typedef __attribute__((address_space(3))) char lds_char_t;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int m = wave + p * W;
+    if (m < NI) {
+      const uint32_t dst = (uint32_t)(uintptr_t)(lds_char_t *)(rbuf + 1024 * m);
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                   :
+                   : "s"(dst), "v"(src[p])
+                   : "memory", "m0");
+    }
+  }
+}
+
+// The prologue of this lane's rows x from operands in registers: the norm weights of its
+// channels (wl, wh) and its rotary values as the record layout lays them out (IL:
+// interleaved (cos, sin) pairs; else cos, then sin). Each layout has its own copy of the
+// arithmetic, so the loaded registers are used as they lie, with no copies.
+template <int D, bool IL>
+__device__ __forceinline__ void prologue_apply(u32x4_t (&x)[D / 32], const f32x4_t (&wl)[D / 32],
+                                                   const f32x4_t (&wh)[D / 32], const f32x4_t (&v0)[D / 32],
+                                                   const f32x4_t (&v1)[D / 32], float eps) {
+  constexpr int KT = D / 32;
+  PrologueOps<D> ops;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ops.w[t][q] = wl[t][q], ops.w[t][4 + q] = wh[t][q];
+      ops.c[t][q] = IL ? (q < 2 ? v0[t][2 * q] : v1[t][2 * q - 4]) : v0[t][q];
+      ops.s[t][q] = IL ? (q < 2 ? v0[t][2 * q + 1] : v1[t][2 * q - 3]) : v1[t][q];
+    }
+  }
+  norm_rope_apply<D>(x, ops, eps);
+}
+// The prologue with its operands from LDS: norm weights, rotary values from record tq of
+// the rope buffer.
+template <int D>
+__device__ __forceinline__ void prologue_lds(u32x4_t (&x)[D / 32], const float *w_lds, const char *rbuf, int tq, int g,
+                                             bool il, float eps) {
+  constexpr int KT = D / 32;
+  typedef __attribute__((address_space(3))) const f32x4_t lds_f32x4_t;
+  const float *rec = reinterpret_cast<const float *>(rbuf) + tq * D;
+  PrologueOps<D> ops;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const f32x4_t lo = *(lds_f32x4_t *)(w_lds + 32 * t + 8 * g);
+    const f32x4_t hi = *(lds_f32x4_t *)(w_lds + 32 * t + 8 * g + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ops.w[t][q] = lo[q], ops.w[t][4 + q] = hi[q];
+    if (il) {  // interleaved records: the lane's pairs lie together
+      const f32x4_t v0 = *(lds_f32x4_t *)(rec + 32 * t + 8 * g);
+      const f32x4_t v1 = *(lds_f32x4_t *)(rec + 32 * t + 8 * g + 4);
+      ops.c[t][0] = v0[0], ops.s[t][0] = v0[1], ops.c[t][1] = v0[2], ops.s[t][1] = v0[3];
+      ops.c[t][2] = v1[0], ops.s[t][2] = v1[1], ops.c[t][3] = v1[2], ops.s[t][3] = v1[3];
+    } else {  // split records: cos, then sin at D / 2
+      const f32x4_t cv = *(lds_f32x4_t *)(rec + 16 * t + 4 * g);
+      const f32x4_t sv = *(lds_f32x4_t *)(rec + D / 2 + 16 * t + 4 * g);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ops.c[t][q] = cv[q], ops.s[t][q] = sv[q];
+    }
+  }
+  norm_rope_apply<D>(x, ops, eps);
+}
+
+// The same prologue with the rotary values read from the table in global memory (the
+// units whose records are not in the rope buffer). Only the two table layouts the direct
+// calls admit (split or interleaved (cos, sin) rows): 16-byte loads of the lane's pairs,
+// issued together with the weights' LDS reads.
+template <int D>
+__device__ __forceinline__ void prologue_global(u32x4_t (&x)[D / 32], const AttnArgs &a, const float *w_lds,
+                                                int64_t rr, int g, bool il) {
+  constexpr int KT = D / 32;
+  typedef __attribute__((address_space(3))) const f32x4_t lds_f32x4_t;
+  asm volatile("" : "+v"(g), "+v"(rr));  // per-lane addresses formed here, not held across the tile loop
+  const float *row_c = a.rope.cos + rr * a.rope.row_stride, *row_s = a.rope.sin + rr * a.rope.row_stride;
+  f32x4_t wl[KT], wh[KT], v0[KT], v1[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const f32x4u_t c0 = *(g_f32x4u_t *)(il ? row_c + 32 * t + 8 * g : row_c + 16 * t + 4 * g);
+    const f32x4u_t c1 = *(g_f32x4u_t *)(il ? row_c + 32 * t + 8 * g + 4 : row_s + 16 * t + 4 * g);
+    v0[t] = f32x4_t{c0[0], c0[1], c0[2], c0[3]};
+    v1[t] = f32x4_t{c1[0], c1[1], c1[2], c1[3]};
+    wl[t] = *(lds_f32x4_t *)(w_lds + 32 * t + 8 * g);
+    wh[t] = *(lds_f32x4_t *)(w_lds + 32 * t + 8 * g + 4);
+  }
+  if (il) {
+    prologue_apply<D, true>(x, wl, wh, v0, v1, a.eps);
+  } else {
+    prologue_apply<D, false>(x, wl, wh, v0, v1, a.eps);
+  }
+}
+
 // One workgroup = R replicas x (W consumer wavefronts + 1 producer wavefront).
 //
 // The producer issues every load of its replica's K/V stream (LDS-DMA into the ring, plus
@@ -1117,7 +1321,7 @@ __device__ __forceinline__ void lds_publish() { asm volatile("s_waitcnt lgkmcnt(
 // tile hands stage i from the producer (its loads complete) to the consumers and stage
 // i-1 back (their reads of it done), and a partial written in iteration t to the
 // producer, who stores it in iteration t + 1.
-template <int LAYOUT, int W, int D, bool F8 = false>
+template <int LAYOUT, int W, int D, bool F8 = false, bool DQ = false>
 __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     const AttnArgs a, const int32_t *__restrict__ table, const int32_t *__restrict__ plan,
     const int32_t *__restrict__ seqlens) {
@@ -1129,19 +1333,56 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   constexpr int R = replicas(W);
   constexpr int S = G::NS;
   constexpr int RBYTES = G::SMEM + O::BYTES;  // per replica: the ring, then the out slot
+  constexpr int SEQ = kernel_seq_cap<D, W, F8, DQ>();  // sequences whose metadata is staged in LDS
+  constexpr int RBUF = QTOK * D * 4;                  // DQ: a replica's rope buffer
   static_assert(S >= 3, "the wait schedule keeps one group between tiles");
   static_assert((S - 2) * G::NI + (S - 2) < 64, "vmcnt holds 6 bits");
+  static_assert(!(DQ && F8), "direct query rows are bf16");
+  static_assert(SEQ >= 1, "LDS budget");
   __shared__ __attribute__((aligned(1024))) char smem_all[R * RBYTES];
-  __shared__ i32x2_t seq_tab[SEQ_LDS + 1];
+  __shared__ i32x2_t seq_tab[SEQ + 1];
+  // DQ: the replicas' rope buffers, the norm weights, (first token, rows) and the rotary
+  // table rows of the first QTOK draft tokens of each sequence.
+  __shared__ __attribute__((aligned(16))) char dq_lds[DQ ? R * RBUF + D * 4 + SEQ * (8 + 4 * QTOK) : 16];
+  char *const rope_bufs = dq_lds;
+  float *const w_tab = reinterpret_cast<float *>(dq_lds + R * RBUF);
+  i32x2_t *const qmeta = reinterpret_cast<i32x2_t *>(dq_lds + R * RBUF + D * 4);
+  int32_t *const rrow = reinterpret_cast<int32_t *>(dq_lds + R * RBUF + D * 4 + SEQ * 8);
   SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens, (lds_i32x2_t *)seq_tab, false};
-  if (sm.var() && a.batch <= SEQ_LDS) {  // uniform: every wavefront takes the barrier
-    for (int j = threadIdx.x; j <= a.batch; j += blockDim.x) {
-      const int len = j < a.batch || a.csr ? seqlens[j] : 0;  // CSR: indptr[j]
-      seq_tab[j] = i32x2_t{plan[j], len};
+  const bool stage_seq = sm.var() && a.batch <= SEQ;
+  if (stage_seq || DQ) {  // uniform: every wavefront takes the barrier (DQ calls have batch <= SEQ)
+    // Every load of a thread's entries issued before any is used: the staging costs one
+    // round trip to memory, two with explicit query positions (token row, then position).
+    const bool pro = DQ && a.qn_w != nullptr;
+    for (int j = threadIdx.x; j <= a.batch || (pro && (j < a.batch * QTOK || j < D)); j += blockDim.x) {
+      int32_t p0 = 0, len = 0, c0 = j * a.q_len, c1 = (j + 1) * a.q_len, b0 = 0, b1 = 0;
+      float wj = 0.f;
+      const int bb = j / QTOK, tt = j - (j / QTOK) * QTOK;
+      if (stage_seq && j <= a.batch) p0 = plan[j], len = j < a.batch || a.csr ? seqlens[j] : 0;  // CSR: indptr[j]
+      if (DQ && j < a.batch && a.cu_q) c0 = a.cu_q[j], c1 = a.cu_q[j + 1];
+      if (pro && j < D) wj = a.qn_w[j];
+      if (pro && j < a.batch * QTOK) {
+        b0 = a.cu_q ? a.cu_q[bb] : bb * a.q_len;
+        b1 = a.cu_q ? a.cu_q[bb + 1] : (bb + 1) * a.q_len;
+      }
+      if (stage_seq && j <= a.batch) seq_tab[j] = i32x2_t{p0, len};
+      if constexpr (DQ) {
+        if (j < a.batch) {
+          int32_t rows = c1 - c0;
+          rows = rows < 0 ? 0 : (rows > a.q_len ? a.q_len : rows);
+          qmeta[j] = i32x2_t{c0, rows};
+        }
+        if (pro && j < D) w_tab[j] = wj;
+        if (pro && j < a.batch * QTOK) {
+          const int64_t tok = (int64_t)b0 + tt;
+          const int64_t pos = tt >= b1 - b0 ? 0 : (a.q_pos ? a.q_pos[tok] : tok);
+          rrow[j] = (int32_t)clamp_row(a.rope, pos);
+        }
+      }
     }
     lds_publish();
     block_sync();
-    sm.staged = true;
+    sm.staged = stage_seq;
   }
   const int lane = threadIdx.x & 63, wv = wave_id();
   const int rep = wv / (W + 1), wave = wv - rep * (W + 1);  // replica; W = the producer
@@ -1275,11 +1516,32 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   int qn_unit = -1;
   u32x4_t qn[QF], qf[QF];
   float rsn = 1.f, sl = a.scale_log2;
-  if (ntiles > 0) {
+  if (!DQ && ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < QF; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
     if (F8) rsn = qscale(cc.u);
     qn_unit = cc.u;
+  }
+  // DQ: this replica's rope buffer; rb_unit: the unit whose records it holds (complete),
+  // dma_unit: the unit whose records this segment brings in (its DMA issued at the
+  // segment's second tile, awaited at its last).
+  char *const rbuf = rope_bufs + rep * RBUF;
+  const bool il = a.rope.pair_stride == 2;
+  int rb_unit = -1, dma_unit = -1;
+  bool dma_issued = false;
+  bool qn_ok = false;
+  if constexpr (DQ) {
+    if (ntiles > 0) {  // the first unit: its rows, and its records before the first barrier
+      if (a.qn_w != nullptr) {
+        rope_records_dma<D, W>(a, (lds_i32_t *)rrow + (cc.u / a.ups) * QTOK, rbuf, wave, lane);
+        rb_unit = cc.u;
+      }
+      const QRowD x = direct_row(a, (lds_i32x2_t *)qmeta, cc.u, wave * 16 + n, g);
+      direct_load_rows(a, x, qn);
+      qn_ok = x.ok;
+      qn_unit = cc.u;
+      wait_vm<0>();
+    }
   }
   f32x4_t acc[G::DB];
   float m = -INFINITY, l = 0.f;
@@ -1287,6 +1549,58 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   for (int i = 0; i < nloop; ++i) {
     block_sync();
     if (i >= ntiles) continue;
+    if constexpr (DQ) {
+    if (i == 0 || cc.lt == 0) {  // a segment starts: its query rows, prologue applied
+      bool ok = qn_ok;
+      int tq = 0;
+      if (qn_unit == cc.u) {
+#pragma unroll
+        for (int t = 0; t < QF; ++t) qf[t] = qn[t];
+        tq = direct_tq(a, cc.u, wave * 16 + n);
+      } else {
+        const QRowD x = direct_row(a, (lds_i32x2_t *)qmeta, cc.u, wave * 16 + n, g);
+        direct_load_rows(a, x, qf);
+        ok = x.ok;
+        tq = x.tq;
+      }
+#pragma unroll
+      for (int t = 0; t < QF; ++t) {
+        asm volatile("" : "+v"(qf[t]));
+        qn[t] = u32x4_t{0, 0, 0, 0};  // consumed: no registers held for it through the prologue
+      }
+      if (a.qn_w != nullptr) {
+        if (rb_unit == cc.u) {
+          prologue_lds<D>(qf, w_tab, rbuf, tq, g, il, a.eps);
+        } else {
+          const int b = cc.u / a.ups;
+          prologue_global<D>(qf, a, w_tab, ((lds_i32_t *)rrow)[b * QTOK + tq], g, il);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < QF; ++t)
+        if (!ok) qf[t] = u32x4_t{0, 0, 0, 0};
+      rb_unit = -1;
+      qn_unit = -1;
+      dma_unit = -1;
+      dma_issued = false;
+      if (cc.u + 1 < units && cc.lt + ntiles - i > cc.tiles) {  // the share reaches unit u + 1
+        const QRowD x = direct_row(a, (lds_i32x2_t *)qmeta, cc.u + 1, wave * 16 + n, g);
+        direct_load_rows(a, x, qn);
+        qn_ok = x.ok;
+        qn_unit = cc.u + 1;
+        if (a.qn_w != nullptr) dma_unit = cc.u + 1;
+      }
+#pragma unroll
+      for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      m = -INFINITY;
+      l = 0.f;
+    } else if (dma_unit >= 0 && !dma_issued) {
+      // Second tile of the segment: every wavefront is past the buffer's reads of the
+      // segment's start (the barrier above), so the next unit's records may come in.
+      rope_records_dma<D, W>(a, (lds_i32_t *)rrow + (dma_unit / a.ups) * QTOK, rbuf, wave, lane);
+      dma_issued = true;
+    }
+    } else {
     if (i == 0 || cc.lt == 0) {  // a segment starts: its query rows
       if (qn_unit == cc.u) {
 #pragma unroll
@@ -1311,8 +1625,15 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       m = -INFINITY;
       l = 0.f;
     }
+    }
     compute_tile<D, F8>(a, stage(i), qf, sl, acc, m, l, cc.lt * G::T, cc.L, lane);
     const bool end = cc.lt == cc.tiles - 1 || i == ntiles - 1;
+    if (DQ && end && dma_issued) {
+      // The next unit's records in place before the barrier that opens it (this
+      // wavefront's own loads: the rows prefetched, then the records' DMA).
+      wait_vm<0>();
+      rb_unit = dma_unit;
+    }
     if (end) {  // the segment ends: its partial
       const float lt_sum = sum_over_groups(l);
       const float inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
@@ -1468,34 +1789,54 @@ __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restri
 
 typedef void (*AttnKernel)(const AttnArgs, const int32_t *, const int32_t *, const int32_t *);
 
-template <int LAYOUT, int D, bool F8>
+template <int LAYOUT, int D, bool F8, bool DQ>
 static AttnKernel pick_kernel(int w) {
   switch (w) {
-    case 1: return attn_fwd_kernel<LAYOUT, 1, D, F8>;
-    case 2: return attn_fwd_kernel<LAYOUT, 2, D, F8>;
-    case 3: return attn_fwd_kernel<LAYOUT, 3, D, F8>;
-    case 4: return attn_fwd_kernel<LAYOUT, 4, D, F8>;
-    case 5: return attn_fwd_kernel<LAYOUT, 5, D, F8>;
-    case 6: return attn_fwd_kernel<LAYOUT, 6, D, F8>;
-    case 7: return attn_fwd_kernel<LAYOUT, 7, D, F8>;
-    default: return attn_fwd_kernel<LAYOUT, 8, D, F8>;
+    case 1: return attn_fwd_kernel<LAYOUT, 1, D, F8, DQ>;
+    case 2: return attn_fwd_kernel<LAYOUT, 2, D, F8, DQ>;
+    case 3: return attn_fwd_kernel<LAYOUT, 3, D, F8, DQ>;
+    case 4: return attn_fwd_kernel<LAYOUT, 4, D, F8, DQ>;
+    case 5: return attn_fwd_kernel<LAYOUT, 5, D, F8, DQ>;
+    case 6: return attn_fwd_kernel<LAYOUT, 6, D, F8, DQ>;
+    case 7: return attn_fwd_kernel<LAYOUT, 7, D, F8, DQ>;
+    default: return attn_fwd_kernel<LAYOUT, 8, D, F8, DQ>;
   }
 }
 
-// F8 (e4m3 K/V): the paged layouts only.
-static AttnKernel select_kernel(int layout, int d, int w, bool f8 = false) {
-  if (f8) {
-    if (d == 128) return layout == PAGED16 ? pick_kernel<PAGED16, 128, true>(w) : pick_kernel<PAGED, 128, true>(w);
-    return layout == PAGED16 ? pick_kernel<PAGED16, 64, true>(w) : pick_kernel<PAGED, 64, true>(w);
+// How a call's consumers get their query rows: straight from the caller's layout with the
+// prologue applied in the kernel (bf16, no verify tokens, q_len <= QTOK, the batch's
+// metadata fits the kernel's LDS, and a small call: at most one unit per two shares), else
+// packed by a query pass (pack_queries_kernel, or pack_queries_f8_kernel for e4m3 K/V).
+enum QMode { Q_DIRECT = 0, Q_PACKED = 1, Q_F8 = 2 };
+
+template <int D>
+static int dq_seq_cap(int w) {
+  switch (w) {
+    case 1: return kernel_seq_cap<D, 1, false, true>();
+    case 2: return kernel_seq_cap<D, 2, false, true>();
+    case 3: return kernel_seq_cap<D, 3, false, true>();
+    case 4: return kernel_seq_cap<D, 4, false, true>();
+    case 5: return kernel_seq_cap<D, 5, false, true>();
+    case 6: return kernel_seq_cap<D, 6, false, true>();
+    case 7: return kernel_seq_cap<D, 7, false, true>();
+    default: return kernel_seq_cap<D, 8, false, true>();
   }
+}
+
+static AttnKernel select_kernel(int layout, int d, int w, int qmode) {
+  if (qmode == Q_F8) {
+    if (d == 128) return layout == PAGED16 ? pick_kernel<PAGED16, 128, true, false>(w) : pick_kernel<PAGED, 128, true, false>(w);
+    return layout == PAGED16 ? pick_kernel<PAGED16, 64, true, false>(w) : pick_kernel<PAGED, 64, true, false>(w);
+  }
+  const bool dq = qmode == Q_DIRECT;
   if (d == 128) {
-    if (layout == CONTIG) return pick_kernel<CONTIG, 128, false>(w);
-    if (layout == PAGED16) return pick_kernel<PAGED16, 128, false>(w);
-    return pick_kernel<PAGED, 128, false>(w);
+    if (layout == CONTIG) return dq ? pick_kernel<CONTIG, 128, false, true>(w) : pick_kernel<CONTIG, 128, false, false>(w);
+    if (layout == PAGED16) return dq ? pick_kernel<PAGED16, 128, false, true>(w) : pick_kernel<PAGED16, 128, false, false>(w);
+    return dq ? pick_kernel<PAGED, 128, false, true>(w) : pick_kernel<PAGED, 128, false, false>(w);
   }
-  if (layout == CONTIG) return pick_kernel<CONTIG, 64, false>(w);
-  if (layout == PAGED16) return pick_kernel<PAGED16, 64, false>(w);
-  return pick_kernel<PAGED, 64, false>(w);
+  if (layout == CONTIG) return dq ? pick_kernel<CONTIG, 64, false, true>(w) : pick_kernel<CONTIG, 64, false, false>(w);
+  if (layout == PAGED16) return dq ? pick_kernel<PAGED16, 64, false, true>(w) : pick_kernel<PAGED16, 64, false, false>(w);
+  return dq ? pick_kernel<PAGED, 64, false, true>(w) : pick_kernel<PAGED, 64, false, false>(w);
 }
 
 struct RowPlan {
@@ -1548,16 +1889,17 @@ struct Sizing {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// tail: a verify call (one more partial slot per unit, for its verify tokens). f8: e4m3 K/V.
+// tail: a verify call (one more partial slot per unit, for its verify tokens). qmode: how
+// the queries reach the consumers (Q_DIRECT needs no packed rows in the workspace).
 static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int max_k,
-                  bool need_plan, Sizing *sz, bool tail = false, bool f8 = false) {
+                  bool need_plan, Sizing *sz, bool tail = false, int qmode = Q_PACKED) {
   DeviceInfo info;
   int rc = device_info(&info);
   if (rc != FM_OK) return rc;
   sz->rp = row_plan(hq / hkv, q_len);
-  AttnKernel k = select_kernel(layout, d, sz->rp.nrb, f8);
+  AttnKernel k = select_kernel(layout, d, sz->rp.nrb, qmode);
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
-  const int tile = f8 ? TILE_F8 : TILE;
+  const int tile = qmode == Q_F8 ? TILE_F8 : TILE;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + tile - 1) / tile);
   const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
   const int r = replicas(sz->rp.nrb);
@@ -1575,10 +1917,10 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   size_t off = 0;
   sz->plan_off = off;
   if (need_plan) off = align256(off + 2 * sizeof(int32_t) * ((size_t)batch + 1));
-  sz->q_off = off;
-  off = align256(off + sizeof(uint16_t) * units * rows * d);
-  sz->rs_off = off;  // fp8 calls: score scale per packed row
-  off = align256(off + sizeof(float) * units * rows);
+  sz->q_off = off;  // packed query rows (none for direct rows); fp8: a score scale per row
+  if (qmode != Q_DIRECT) off = align256(off + sizeof(uint16_t) * units * rows * d);
+  sz->rs_off = off;
+  if (qmode == Q_F8) off = align256(off + sizeof(float) * units * rows);
   sz->lse_off = off;
   off = align256(off + 2 * sizeof(float) * slots * rows);
   sz->o_off = off;
@@ -1645,12 +1987,36 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     a.col_last = (uint32_t)(a.table_width - 1 < 0x7fffffffll ? a.table_width - 1 : 0x7fffffffll);
     a.page_last = (uint32_t)(a.num_pages - 1 < 0xffffffffll ? a.num_pages - 1 : 0xffffffffll);
   }
-  // e4m3 K/V run on tiles of TILE_F8 positions: they always plan for themselves (a
-  // caller's plan counts TILE-position tiles).
+  // A plan made here (none given) holds both tile prefixes (bf16 and e4m3 tiles).
   const bool need_plan = a.seqlens != nullptr && c.plan == nullptr;
+  int qmode = a.f8 ? Q_F8 : Q_PACKED;
   Sizing sz;
-  int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, a.f8 != 0);
+  int rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, qmode);
   if (rc != FM_OK) return rc;
+  if (!a.f8 && vf == nullptr && c.q_len <= QTOK) {
+    const RowPlan rp = row_plan(c.hq / c.hkv, c.q_len);
+    // Rotary rows read in 16-byte chunks: split cos / sin rows (both 16-byte aligned) or
+    // interleaved (cos, sin) rows (sin = cos + 1, the row 16-byte aligned).
+    const bool split = c.rope_ps == 1 && ((uintptr_t)c.rope_sin & 15) == 0;
+    const bool inter = c.rope_ps == 2 && c.rope_sin == c.rope_cos + 1;
+    const bool fast_rope = c.qn_w == nullptr || ((split || inter) && ((uintptr_t)c.rope_cos & 15) == 0 &&
+                                                 c.rope_rs % 4 == 0 && ((uintptr_t)c.qn_w & 3) == 0);
+    const int cap = c.d == 128 ? dq_seq_cap<128>(rp.nrb) : dq_seq_cap<64>(rp.nrb);
+    // Direct rows cost a prologue at every segment start, inside the workgroup's barrier
+    // cycle (about 1.5 us per segment measured at 64 rows x D 128); the query pass costs a
+    // launch and one read + write of the rows. Direct wins when every share holds about one
+    // segment: units <= shares / 2 (a batch-1 call), and loses on full batches (C3's 512
+    // units over 512 shares: 184 us kernel against 165 + 8.5 us). FLASHMAP_QUERY_PASS=1
+    // forces the pass, =0 the direct rows where they apply; both give the same bits.
+    const int force = env_int("FLASHMAP_QUERY_PASS", -1);
+    const int64_t units = (int64_t)c.batch * c.hkv * rp.rgroups;
+    const bool small = units * 2 <= sz.num_shares;
+    if (fast_rope && c.batch <= cap && (force == 0 || (force < 0 && small))) qmode = Q_DIRECT;
+  }
+  if (qmode == Q_DIRECT) {
+    rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, qmode);
+    if (rc != FM_OK) return rc;
+  }
   if (c.static_ws && sz.bytes > c.ws_bytes)
     return fail(FM_ERR_WORKSPACE,
                 "this call needs %zu bytes of scratch; the library's static scratch holds %zu bytes "
@@ -1702,20 +2068,23 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   const int64_t qblocks = (units * sz.rp.nrb + 3) / 4;
   const VerifyArgs nov{};
-  if (a.f8 && c.d == 128)
+  if (qmode == Q_DIRECT) {
+    // no query pass: the attention kernel reads the rows and applies the prologue
+  } else if (a.f8 && c.d == 128) {
     pack_queries_f8_kernel<128><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
-  else if (a.f8)
+  } else if (a.f8) {
     pack_queries_f8_kernel<64><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
-  else if (vf != nullptr && c.d == 128)
+  } else if (vf != nullptr && c.d == 128) {
     pack_queries_kernel<128, true><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, *vf);
-  else if (vf != nullptr)
+  } else if (vf != nullptr) {
     pack_queries_kernel<64, true><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, *vf);
-  else if (c.d == 128)
+  } else if (c.d == 128) {
     pack_queries_kernel<128, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
-  else
+  } else {
     pack_queries_kernel<64, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
-  FM_CHECK_HIP(hipGetLastError());
-  AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb, a.f8 != 0);
+  }
+  if (qmode != Q_DIRECT) FM_CHECK_HIP(hipGetLastError());
+  AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb, qmode);
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
@@ -1767,7 +2136,7 @@ extern "C" size_t fm_attn_workspace_bytes(int32_t batch, int32_t max_seqlen_q, i
     const int layout = v < 3 ? v : v - 2;
     Sizing sz;
     rc = sizing(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, max_seqlen_k,
-                true, &sz, false, v >= 3);
+                true, &sz, false, v >= 3 ? Q_F8 : Q_PACKED);
     if (rc == FM_OK && sz.bytes > bytes) bytes = sz.bytes;
   }
   if (device != prev) hipSetDevice(prev);
@@ -2027,7 +2396,7 @@ extern "C" size_t fm_verify_workspace_bytes(int32_t batch, int32_t verify_len, i
   if (device != prev && hipSetDevice(device) != hipSuccess) return 0;
   Sizing sz;
   const int rc = sizing(PAGED, batch, verify_len, num_q_heads, num_kv_heads, head_dim,
-                        verify_max_context(max_context, pool_size), true, &sz, true);
+                        verify_max_context(max_context, pool_size), true, &sz, true, Q_PACKED);
   if (device != prev) hipSetDevice(prev);
   return rc == FM_OK ? sz.bytes : 0;
 }

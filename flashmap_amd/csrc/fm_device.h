@@ -132,9 +132,7 @@ __device__ __forceinline__ int64_t clamp_row(const Rope &rope, int64_t r) {
 
 // The per-lane operands of the prologue for one row in the row-quad layout (x[t] holds
 // channels 32 t + 8 g + (0..7), i.e. the pairs 16 t + 4 g + (0..3)): the norm weights
-// of those channels and the rotary cos / sin of those pairs. Loaded with 16-byte loads
-// where the table layout allows (contiguous pairs, or (cos, sin) interleaved), else per
-// element.
+// of those channels and the rotary cos / sin of those pairs.
 template <int D>
 struct PrologueOps {
   float w[D / 32][8];
@@ -142,28 +140,22 @@ struct PrologueOps {
 };
 
 typedef __attribute__((ext_vector_type(4), aligned(4))) float f32x4u_t;  // 4-byte aligned
+typedef __attribute__((address_space(1))) const f32x4u_t g_f32x4u_t;     // global memory
+typedef __attribute__((address_space(1))) const float g_cfloat_t;
 
+// The rotary cos / sin of this lane's pairs at table row rope_row into ops.c / ops.s, with
+// global loads (they count on vmcnt only, never on the LDS counter): 16-byte loads where
+// the table layout allows (contiguous pairs, or (cos, sin) interleaved), else per element.
 template <int D>
-__device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const float *__restrict__ w,
-                                                  const Rope &rope, int64_t rope_row, int g) {
+__device__ __forceinline__ void load_rope_ops(PrologueOps<D> &ops, const Rope &rope, int64_t rope_row, int g) {
   constexpr int KT = D / 32;
-#pragma unroll
-  for (int t = 0; t < KT; ++t) {
-    const f32x4u_t lo = *reinterpret_cast<const f32x4u_t *>(w + 32 * t + 8 * g);
-    const f32x4u_t hi = *reinterpret_cast<const f32x4u_t *>(w + 32 * t + 8 * g + 4);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ops.w[t][q] = lo[q];
-      ops.w[t][4 + q] = hi[q];
-    }
-  }
   const float *cs = rope.cos + rope_row * rope.row_stride;
   const float *sn = rope.sin + rope_row * rope.row_stride;
   if (rope.pair_stride == 1) {
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      const f32x4u_t cv = *reinterpret_cast<const f32x4u_t *>(cs + 16 * t + 4 * g);
-      const f32x4u_t sv = *reinterpret_cast<const f32x4u_t *>(sn + 16 * t + 4 * g);
+      const f32x4u_t cv = *(g_f32x4u_t *)(cs + 16 * t + 4 * g);
+      const f32x4u_t sv = *(g_f32x4u_t *)(sn + 16 * t + 4 * g);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         ops.c[t][q] = cv[q];
@@ -173,8 +165,8 @@ __device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const flo
   } else if (rope.pair_stride == 2 && sn == cs + 1) {
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      const f32x4u_t v0 = *reinterpret_cast<const f32x4u_t *>(cs + 32 * t + 8 * g);
-      const f32x4u_t v1 = *reinterpret_cast<const f32x4u_t *>(cs + 32 * t + 8 * g + 4);
+      const f32x4u_t v0 = *(g_f32x4u_t *)(cs + 32 * t + 8 * g);
+      const f32x4u_t v1 = *(g_f32x4u_t *)(cs + 32 * t + 8 * g + 4);
       ops.c[t][0] = v0[0], ops.s[t][0] = v0[1], ops.c[t][1] = v0[2], ops.s[t][1] = v0[3];
       ops.c[t][2] = v1[0], ops.s[t][2] = v1[1], ops.c[t][3] = v1[2], ops.s[t][3] = v1[3];
     }
@@ -184,10 +176,43 @@ __device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const flo
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t p = 16 * t + 4 * g + q;
-        ops.c[t][q] = cs[p * rope.pair_stride];
-        ops.s[t][q] = sn[p * rope.pair_stride];
+        ops.c[t][q] = *(g_cfloat_t *)(cs + p * rope.pair_stride);
+        ops.s[t][q] = *(g_cfloat_t *)(sn + p * rope.pair_stride);
       }
   }
+}
+
+template <int D>
+__device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const float *__restrict__ w,
+                                                  const Rope &rope, int64_t rope_row, int g) {
+  constexpr int KT = D / 32;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const f32x4u_t lo = *(g_f32x4u_t *)(w + 32 * t + 8 * g);
+    const f32x4u_t hi = *(g_f32x4u_t *)(w + 32 * t + 8 * g + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ops.w[t][q] = lo[q];
+      ops.w[t][4 + q] = hi[q];
+    }
+  }
+  load_rope_ops<D>(ops, rope, rope_row, g);
+}
+
+// fp32 products, sums and differences each rounded on its own: never contracted into a
+// fused multiply-add, whichever kernel inlines them (the prologue's bits must not depend
+// on the surrounding code: the fused and the standalone prologue agree bit for bit).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
 }
 
 // RMSNorm (scale rounded to bf16 before the multiply, product rounded to bf16) then
@@ -209,23 +234,23 @@ __device__ __forceinline__ void norm_rope_apply(u32x4_t (&x)[D / 32], const Prol
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float e = bf16_lo(x[t][q]), o = bf16_hi(x[t][q]);
-      ss = __fadd_rn(ss, __fmul_rn(e, e));
-      ss = __fadd_rn(ss, __fmul_rn(o, o));
+      ss = add_rn(ss, mul_rn(e, e));
+      ss = add_rn(ss, mul_rn(o, o));
     }
   }
   ss = sum_over_groups(ss);
-  const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+  const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, (float)D), eps)));
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float se = round_bf16(__fmul_rn(ops.w[t][2 * q], r));
-      const float so = round_bf16(__fmul_rn(ops.w[t][2 * q + 1], r));
-      const float e = round_bf16(__fmul_rn(bf16_lo(x[t][q]), se));
-      const float o = round_bf16(__fmul_rn(bf16_hi(x[t][q]), so));
+      const float se = round_bf16(mul_rn(ops.w[t][2 * q], r));
+      const float so = round_bf16(mul_rn(ops.w[t][2 * q + 1], r));
+      const float e = round_bf16(mul_rn(bf16_lo(x[t][q]), se));
+      const float o = round_bf16(mul_rn(bf16_hi(x[t][q]), so));
       const float c = ops.c[t][q], s = ops.s[t][q];
-      const float e2 = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s));
-      const float o2 = __fadd_rn(__fmul_rn(o, c), __fmul_rn(e, s));
+      const float e2 = sub_rn(mul_rn(e, c), mul_rn(o, s));
+      const float o2 = add_rn(mul_rn(o, c), mul_rn(e, s));
       x[t][q] = pack_bf16x2(e2, o2);
     }
   }
@@ -246,27 +271,27 @@ __device__ __forceinline__ void norm_rope_f32(const u32x4_t (&x)[D / 32], const 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float e = bf16_lo(x[t][q]), o = bf16_hi(x[t][q]);
-      ss = __fadd_rn(ss, __fmul_rn(e, e));
-      ss = __fadd_rn(ss, __fmul_rn(o, o));
+      ss = add_rn(ss, mul_rn(e, e));
+      ss = add_rn(ss, mul_rn(o, o));
     }
   }
   ss = sum_over_groups(ss);
-  const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+  const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(ss, (float)D), eps)));
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       float e, o;
       if constexpr (SGL) {
-        e = round_bf16(__fmul_rn(__fmul_rn(bf16_lo(x[t][q]), r), ops.w[t][2 * q]));
-        o = round_bf16(__fmul_rn(__fmul_rn(bf16_hi(x[t][q]), r), ops.w[t][2 * q + 1]));
+        e = round_bf16(mul_rn(mul_rn(bf16_lo(x[t][q]), r), ops.w[t][2 * q]));
+        o = round_bf16(mul_rn(mul_rn(bf16_hi(x[t][q]), r), ops.w[t][2 * q + 1]));
       } else {
-        e = round_bf16(__fmul_rn(bf16_lo(x[t][q]), round_bf16(__fmul_rn(ops.w[t][2 * q], r))));
-        o = round_bf16(__fmul_rn(bf16_hi(x[t][q]), round_bf16(__fmul_rn(ops.w[t][2 * q + 1], r))));
+        e = round_bf16(mul_rn(bf16_lo(x[t][q]), round_bf16(mul_rn(ops.w[t][2 * q], r))));
+        o = round_bf16(mul_rn(bf16_hi(x[t][q]), round_bf16(mul_rn(ops.w[t][2 * q + 1], r))));
       }
       const float c = ops.c[t][q], s = ops.s[t][q];
-      y[t][2 * q] = __fsub_rn(__fmul_rn(e, c), __fmul_rn(o, s));
-      y[t][2 * q + 1] = __fadd_rn(__fmul_rn(o, c), __fmul_rn(e, s));
+      y[t][2 * q] = sub_rn(mul_rn(e, c), mul_rn(o, s));
+      y[t][2 * q + 1] = add_rn(mul_rn(o, c), mul_rn(e, s));
     }
   }
 }

@@ -313,3 +313,64 @@ def test_write_context_kv_pool_sglang(dev):
     for got, exp in zip(dk + dv, wk + wv):
         assert (got.cpu() == exp).float().mean().item() > 0.99
         assert (got.cpu().float() - exp.float()).abs().max().item() <= 2e-2
+
+
+# ------------------------------------------- query rows: direct (in-kernel prologue) vs pass
+
+
+def _tables(kind, rows, d):
+    table = ref.rope_table(rows, d, 1e6)
+    if kind == "interleaved":
+        return table, ops().rope_from_table
+    if kind == "cat":  # [cos | sin] rows
+        return table, lambda t: ops().rope_from_cat(torch.cat([t[..., 0], t[..., 1]], dim=-1).contiguous())
+    return table, lambda t: ops().rope_from_split(t[..., 0].contiguous(), t[..., 1].contiguous())
+
+
+@pytest.mark.parametrize("kind", ["interleaved", "cat", "split"])
+@pytest.mark.parametrize("layout", ["contig", "paged"])
+def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
+    """The attention kernel applies the prologue to the caller's rows itself (direct rows)
+    or reads rows a separate query pass normed and rotated: the same bits either way,
+    for every rotary table layout, with ragged draft rows (cu_seqlens_q shorter than q_len)."""
+    g = gen(41)
+    hq, hkv, d, t, page = 32, 8, 128, 16, 16
+    lens = torch.tensor([700, 33, 1, 260])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q_pre = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table, make = _tables(kind, lmax + t + 1, d)
+    rope = make(table.to(dev))
+    rows = torch.tensor([16, 9, 16, 3]) if layout == "paged" else torch.full((b,), t)
+    cu = torch.cat([torch.zeros(1, dtype=torch.int32), rows.cumsum(0).to(torch.int32)])
+    pos = torch.cat([int(n) + torch.arange(int(r)) for n, r in zip(lens, rows)])
+    n_tok = int(cu[-1])
+    o = ops()
+    pro = o.Prologue(w.to(dev), rope, pos.to(dev), 1e-6)
+    if layout == "paged":
+        bt, total = paged_layout(lens, page, g)
+        cache = vllm_cache_from_contig(k, v, lens, page, bt, total).to(dev)
+
+        def run():
+            return o.block_attention_paged(q_pre[:n_tok].to(dev), cache, cu.to(dev), lens.to(dev, torch.int32),
+                                           bt.to(dev), t, lmax, d ** -0.5, prologue=pro)
+    else:
+        def run():
+            return o.block_attention_contig(q_pre.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev),
+                                            seqlens_k=lens.to(dev), prologue=pro)
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("FLASHMAP_QUERY_PASS", mode)
+        outs[mode] = run()
+    assert torch.equal(outs["0"], outs["1"]), f"{kind}/{layout}: direct rows differ from the query pass"
+    qn = ref.rms_norm_rope_vllm(q_pre[:n_tok], w, table, pos, 1e-6)
+    got = outs["0"].cpu().view(-1, hq, d)
+    for i in range(b):
+        s, e = int(cu[i]), int(cu[i + 1])
+        if layout == "contig":
+            s, e = i * t, (i + 1) * t
+        want = ref.attention(qn[s:e].transpose(0, 1), k[i, :, : int(lens[i])], v[i, :, : int(lens[i])])
+        check_close(got[s:e], want.transpose(0, 1))
