@@ -28,7 +28,8 @@ from . import ops
 
 __all__ = ["ContextCachePlan", "attend_by_segments", "cross_attention_by_segments", "plan_context_cache"]
 
-# FLASHMAP_CONTEXT_CACHE: "auto" (virtual on hybrid targets), "layers" or "virtual".
+# Values of FLASHMAP_CONTEXT_CACHE. "layers": one cache per DiT layer; "virtual": DiT
+# heads packed into the target's own caches; "auto": virtual only beside a hybrid target.
 MODES = ("auto", "layers", "virtual")
 
 
@@ -96,7 +97,7 @@ def plan_context_cache(
     elements are a whole number of DiT heads, and room for every DiT head."""
     mode = mode or os.environ.get("FLASHMAP_CONTEXT_CACHE", "auto")
     if mode not in MODES:
-        raise ValueError(f"FLASHMAP_CONTEXT_CACHE must be one of {MODES}, got {mode!r}")
+        raise ValueError(f"unknown context-cache mode {mode!r} (FLASHMAP_CONTEXT_CACHE takes {', '.join(MODES)})")
 
     def per_layer(reason: str) -> ContextCachePlan:
         return ContextCachePlan(num_layers, heads, num_layers, heads, False, reason)
@@ -164,10 +165,25 @@ def cross_attention_by_segments(
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """:func:`attend_by_segments` with ``flashmap_vllm::paged_cross_attention`` as the
-    per-run call, in one launch over every run of the layer (bf16 caches; the virtual
-    layout is not used with fp8 caches). ``scheduler_metadata``: the step's plan from
+    per-run call, in one launch per ``ops.MAX_RUNS`` runs of the layer (bf16 caches; the
+    virtual layout is not used with fp8 caches). A layer of more runs is attended in
+    consecutive head ranges, each launch reading and writing its range of query and
+    output heads in place. ``scheduler_metadata``: the step's plan from
     ``cross_attention_schedule(seqused_k)``."""
-    _group(query, segments)
-    return ops.block_attention_paged_runs(query, caches, segments, cu_seqlens_q, seqused_k, block_table,
-                                          max_seqlen_q, max_seqlen_k, softmax_scale, prologue=prologue,
-                                          plan=scheduler_metadata, out=out)
+    group = _group(query, segments)
+    if len(segments) <= ops.MAX_RUNS:
+        return ops.block_attention_paged_runs(query, caches, segments, cu_seqlens_q, seqused_k, block_table,
+                                              max_seqlen_q, max_seqlen_k, softmax_scale, prologue=prologue,
+                                              plan=scheduler_metadata, out=out)
+    if out is None:
+        out = torch.empty(query.shape, dtype=torch.bfloat16, device=query.device)
+    for i in range(0, len(segments), ops.MAX_RUNS):
+        chunk = segments[i:i + ops.MAX_RUNS]
+        h0 = chunk[0][3]
+        h1 = h0 + sum(run[2] for run in chunk)
+        rebased = [(c, slot, count, head - h0) for c, slot, count, head in chunk]
+        heads = slice(group * h0, group * h1)
+        ops.block_attention_paged_runs(query[:, heads], caches, rebased, cu_seqlens_q, seqused_k, block_table,
+                                       max_seqlen_q, max_seqlen_k, softmax_scale, prologue=prologue,
+                                       plan=scheduler_metadata, out=out[:, heads])
+    return out

@@ -13,9 +13,10 @@
 // (x as int32, negatives folded by ~x) * 4.6566127342e-10f; a normal is
 // sqrt(-2 log(max(u1, 1e-7))) * cos(6.2831855f * u2) of the first two words.
 //
-// Selection: one 256-thread workgroup per (tile of 8192 logits, row) streams the tile with
+// Selection: one 256-thread workgroup per (tile of logits, row) streams the tile with
 // 16-byte loads, keys it in registers (no noise buffer) and reduces (key, index) over the
-// wavefront and then the workgroup; a one-wavefront-per-row pass merges the tiles. NaN
+// wavefront and then the workgroup; a one-wavefront-per-row pass merges the tiles. Tiles
+// are 16384 logits for the argmax and 8192 for the sampler (SEL_TILE_*, below). NaN
 // counts as the largest key, the first NaN winning (torch.argmax's rule).
 #include <math.h>
 #include <stdint.h>

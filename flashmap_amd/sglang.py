@@ -10,8 +10,10 @@ and the plain functions :func:`rope_freqs` (flashmap/sglang/model.py:116-123),
 :func:`cross_attention_schedule` (the per-step plan in place of
 ``get_scheduler_metadata``, flashmap/sglang/model.py:189-204) and
 :func:`fused_kv_norm_rope_write`, the bf16 pool write the plugin takes from sglang
-(called at flashmap/sglang/model.py:746-766, interleaved RoPE). Registration is
-explicit and idempotent. Not implemented: the e4m3 pool variants.
+(called at flashmap/sglang/model.py:746-766, interleaved RoPE), with the e4m3 pool
+variants ``paged_cross_attention_fp8`` (flashmap/sglang/model.py:154-186) and
+``kv_norm_rope_write_fp8`` (flashmap/sglang/kernels.py:283-357). Registration is
+explicit and idempotent.
 """
 
 from __future__ import annotations

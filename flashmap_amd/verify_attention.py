@@ -35,10 +35,10 @@ class SplitKVVerify:
     buffer is kept, as captured graphs still point at it."""
 
     MAX_SCRATCH_BYTES = 512 << 20
-    # Custom masks arrive as each request's L x L block (EAGLE's QLEN_ONLY) rather than
-    # sglang's full context + L rows. Whoever builds the masks sets this before graphs
-    # are captured; extend_attention_fwd cannot read that layout, so a batch this class
-    # declines then raises instead of falling back.
+    # True when the caller's custom masks hold only the verify tokens' L x L block per
+    # request (EAGLE's QLEN_ONLY layout), not a row over context + L. Set once, before
+    # any graph capture. The fallback extend_attention_fwd reads only the long layout,
+    # so with this set a declined masked batch is an error, not a fall-back.
     qlen_mask = False
 
     def __init__(self):
@@ -87,7 +87,8 @@ class SplitKVVerify:
                             sliding_window_size, sinks, xai_temperature_len)
         if not handled and custom_mask is not None and self.qlen_mask:
             raise RuntimeError(
-                "split-KV verify declined a batch whose mask only it can read (QLEN_ONLY layout)"
+                "this verify batch carries L x L masks (qlen_mask) but cannot run on the split-KV kernel, and "
+                "extend_attention_fwd does not read that mask layout"
             )
         return handled
 

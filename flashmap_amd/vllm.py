@@ -112,15 +112,17 @@ def paged_cross_attention_runs(
 ) -> torch.Tensor:
     """:func:`paged_cross_attention` of one DiT layer whose KV heads lie in runs over
     several bf16 caches (``ContextCachePlan.segments[layer]`` flattened, four ints per
-    run: cache, first slot, count, first head), in one launch; the output is what
-    attend_by_segments concatenates from one call per run
+    run: cache, first slot, count, first head), in one launch per ``ops.MAX_RUNS`` runs;
+    the output is what attend_by_segments concatenates from one call per run
     (flashmap/vllm/context_cache.py:120-139)."""
+    from .context_cache import cross_attention_by_segments
+
     if len(runs) % 4:
         raise ValueError("runs must hold four ints per run (cache, first slot, count, first head)")
     segments = [tuple(runs[i:i + 4]) for i in range(0, len(runs), 4)]
-    return ops.block_attention_paged_runs(
+    return cross_attention_by_segments(
         query, kv_caches, segments, cu_seqlens_q, seqused_k, block_table, max_seqlen_q, max_seqlen_k,
-        softmax_scale, plan=_plan(scheduler_metadata, seqused_k.shape[0]),
+        softmax_scale, scheduler_metadata=_plan(scheduler_metadata, seqused_k.shape[0]),
     )
 
 

@@ -86,3 +86,28 @@ def test_runs_with_fused_prologue_and_plugin_op(dev):
     torch.cuda.synchronize()
     assert torch.equal(fused, plain)
     assert torch.equal(op, plain)
+
+
+def test_more_runs_than_one_launch_takes(dev):
+    """A layer of 10 runs (20 heads in caches of 2) is attended in launches of at most
+    ops.MAX_RUNS runs over consecutive head ranges: each range against the oracle, and
+    the whole layer equal to per-run calls' concatenation within the same bar."""
+    from flashmap_amd import vllm as fv
+
+    layers, heads, hpc, group, d, page = 2, 20, 2, 2, 64, 16
+    print(f"runs layers={layers} heads={heads} hpc={hpc} group={group} (10 runs per layer)", flush=True)
+    plan, caches, q, cu, lens, bt = _case(layers, heads, hpc, group, d, page, 31)
+    gc = [c.to(dev) for c in caches]
+    qd, cud, lensd, btd = q.to(dev), cu.to(dev), lens.to(dev), bt.to(dev)
+    scale = d ** -0.5
+    fv.register()
+    for layer, runs in enumerate(plan.segments):
+        assert len(runs) > ops.MAX_RUNS
+        got = cc.cross_attention_by_segments(qd, gc, runs, cud, lensd, btd, 16, 400, scale)
+        flat = [x for run in runs for x in run]
+        op = torch.ops.flashmap_vllm.paged_cross_attention_runs(qd, gc, flat, cud, lensd, btd, None, 16, 400, scale)
+        torch.cuda.synchronize()
+        want = ref.block_attention_paged_segments(q, caches, runs, cu, lens, bt, scale)
+        check_close(got, want)
+        assert torch.equal(op, got)
+        assert torch.count_nonzero(got[16:32]) == 0

@@ -61,7 +61,7 @@ def test_qlen_mask_decline_raises():
     fwd.qlen_mask = True
     args = _args()
     args[9] = torch.ones(2 * 9, dtype=torch.bool)
-    with pytest.raises(RuntimeError, match="QLEN_ONLY"):
+    with pytest.raises(RuntimeError, match="L x L masks"):
         fwd(*args, logit_cap=30.0)
 
 
