@@ -20,6 +20,7 @@ from ._native import call
 
 __all__ = [
     "Rope",
+    "adaln_residual",
     "argmax_rows",
     "attention_plan",
     "block_attention_contig",
@@ -1113,6 +1114,82 @@ def seeded_normal(
     call("fm_seeded_normal", _i64(seeds).data_ptr(), r.data_ptr(), int(r.dtype == torch.int64), p.data_ptr(),
          int(p.dtype == torch.int64), n, n_cols, float(scale), out.data_ptr(), out.stride(0), _stream(rows))
     return out
+
+
+# --------------------------------------------------------------------- DiT stream
+
+
+def _rows2d(t: torch.Tensor, dim: int, name: str) -> torch.Tensor:
+    """``t (..., dim)`` bf16 as ``(rows, dim)`` rows with unit channel stride (a view
+    when the leading dims flatten to one row stride, else a copy)."""
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.shape[-1] != dim:
+        raise ValueError(f"{name} rows hold {t.shape[-1]} values, expected {dim}")
+    r = t.reshape(-1, dim)
+    if r.stride(-1) != 1 or r.stride(0) % 8 or r.data_ptr() % 16:
+        r = r.contiguous()
+    return r
+
+
+def _vec(t: torch.Tensor, dim: int, name: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.numel() != dim:
+        raise ValueError(f"{name} holds {t.numel()} values, expected {dim} (one per channel)")
+    v = t.reshape(dim)
+    return v if (v.stride(0) == 1 and v.data_ptr() % 16 == 0) else v.contiguous()
+
+
+def adaln_residual(
+    x: torch.Tensor,
+    y: torch.Tensor | None,
+    gate: torch.Tensor | None,
+    modulation: tuple[torch.Tensor, torch.Tensor] | None,
+    eps: float,
+    x_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """The DiT's residual stream in one pass: ``x' = x + gate * y`` (skipped when ``y``
+    is None), then ``h = LN(x') * (1 + scale) + shift`` for ``modulation = (scale,
+    shift)`` (skipped when None), each op rounded to bf16 like torch's eager ops
+    (flashmap/modeling_flashmap.py:114-117, 185-192). ``x``/``y (..., dim)`` bf16;
+    ``gate``, ``scale``, ``shift``: ``dim`` values shared by every row. ``x_out`` (may
+    be ``x``) receives ``x'``, else a new tensor does. Returns ``(x', h)``, ``x'`` None
+    without a residual."""
+    _check_cuda(x, y, gate, x_out, *(modulation or ()))
+    dim = x.shape[-1]
+    if dim % 8 or not 0 < dim <= 8192:
+        raise ValueError(f"rows of {dim} values: the kernel takes a multiple of 8, at most 8192")
+    xr = _rows2d(x, dim, "x")
+    rows = xr.shape[0]
+    yr = g = xo = None
+    if y is not None:
+        if gate is None:
+            raise ValueError("a residual needs its gate")
+        if y.numel() != x.numel():
+            raise ValueError(f"y holds {y.numel()} values, x {x.numel()}")
+        yr, g = _rows2d(y, dim, "y"), _vec(gate, dim, "gate")
+        if x_out is None:
+            x_out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+        if x_out.numel() != x.numel():
+            raise ValueError(f"x_out holds {x_out.numel()} values, x {x.numel()}")
+        xo = x_out.view(rows, dim)  # raises unless x_out's rows are one strided view
+        if xo.stride(-1) != 1 or xo.stride(0) % 8 or xo.data_ptr() % 16:
+            raise ValueError("x_out must hold 16-byte aligned rows with unit channel stride")
+    h = sc = sh = None
+    if modulation is not None:
+        sc, sh = (_vec(m, dim, n) for m, n in zip(modulation, ("scale", "shift")))
+        h = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    if rows == 0 or (yr is None and h is None):
+        return x_out, h
+    hr = None if h is None else h.view(rows, dim)
+    call(
+        "fm_adaln_residual",
+        xr.data_ptr(), xr.stride(0), _ptr(yr), 0 if yr is None else yr.stride(0), _ptr(g), _ptr(sc), _ptr(sh),
+        _ptr(xo), 0 if xo is None else xo.stride(0), _ptr(hr), 0 if hr is None else hr.stride(0),
+        rows, dim, float(eps), _stream(x),
+    )
+    return x_out, h
 
 
 def default_scale(head_dim: int) -> float:

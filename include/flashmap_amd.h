@@ -408,6 +408,22 @@ int fm_seeded_normal(const int64_t *seeds, const void *rows, int32_t rows_int64,
                      void *stream);
 
 /* ---------------------------------------------------------------------------------
+ * f3: the DiT's residual stream between sublayers. Replaces the eager ops of
+ * FlashMapAdaLayerNorm.forward and the gated residuals of FlashMapLayer.forward
+ * (flashmap/modeling_flashmap.py:114-117, 185-192):
+ *   x' = x + gate * y                          (when y is non-NULL; else x' = x)
+ *   h  = LN(x') * (1 + scale) + shift          (when scale is non-NULL)
+ * with every op rounded to bf16 as torch's eager bf16 ops round; LN has no affine
+ * weights (biased variance, eps inside the rsqrt). x, y, x_out, h_out: (rows, dim) bf16
+ * with row strides (elements, multiples of 8); gate, scale, shift: (dim,) bf16 shared by
+ * all rows; x_out may alias x. dim a multiple of 8, at most 8192.
+ */
+int fm_adaln_residual(const void *x, int64_t x_stride, const void *y, int64_t y_stride,
+                      const void *gate, const void *scale, const void *shift, void *x_out,
+                      int64_t x_out_stride, void *h_out, int64_t h_out_stride, int64_t rows,
+                      int32_t dim, float eps, void *stream);
+
+/* ---------------------------------------------------------------------------------
  * Measurement hook. No reference counterpart: it lets a benchmark time the main
  * split-KV attention kernel alone with HIP events on the stream it runs on, without
  * changing the work any call does. While enabled, every attention call records an

@@ -2,10 +2,11 @@
 
 - ``draft`` against the reference's own outputs on two tiny random-init drafters
   (tests/golden/drafter_tiny.safetensors, written from flashmap/modeling_flashmap.py by
-  tests/golden/make_drafter_golden.py): logits within 2 % of the largest logit (max) and
-  0.5 % of the mean logit (mean), the -inf pattern of a state vocabulary exact, and the
-  greedy draft tokens
-  equal wherever the reference's top-2 margin exceeds twice the observed error.
+  tests/golden/make_drafter_golden.py): logits within 0.8 % of the largest logit (max;
+  one bf16 ulp of the largest logits is 0.4-0.8 %) and 0.1 % of the mean logit (mean),
+  the -inf pattern of a state vocabulary exact, and the greedy draft tokens equal on
+  every slot whose reference top-2 margin exceeds twice the observed error -- at least
+  85 % of the slots (the others are within bf16 rounding of a tie).
 - ``spec_generate`` at temperature 0 is lossless: it returns the target's own greedy
   decoding (the property flashmap/modeling_flashmap.py:525-528 states), on a tiny
   random-init Qwen3 target.
@@ -53,14 +54,16 @@ def test_draft_matches_reference(dev, name):
     assert torch.equal(finite, torch.isfinite(got))
     err = (got[finite] - want[finite]).abs()
     scale = want[finite].abs()
-    assert err.max() <= 0.02 * scale.max(), f"max err {err.max():.4f} vs max |logit| {scale.max():.4f}"
-    assert err.mean() <= 0.005 * scale.mean(), f"mean err {err.mean():.5f} vs mean |logit| {scale.mean():.5f}"
+    assert err.max() <= 0.008 * scale.max(), f"max err {err.max():.4f} vs max |logit| {scale.max():.4f}"
+    assert err.mean() <= 0.001 * scale.mean(), f"mean err {err.mean():.5f} vs mean |logit| {scale.mean():.5f}"
     top2 = want.masked_fill(~finite, float("-inf")).topk(2, dim=-1).values
     clear = (top2[..., 0] - top2[..., 1]) > 2 * err.max()
+    same = got.argmax(-1) == want.argmax(-1)
     print(f"{name}: max err {err.max():.4f} (max |logit| {scale.max():.4f}), mean err {err.mean():.5f} "
-          f"(mean |logit| {scale.mean():.4f}), clear-margin slots {clear.float().mean():.2f}", flush=True)
-    assert clear.float().mean() > 0.5
-    assert torch.equal(got.argmax(-1)[clear], want.argmax(-1)[clear])
+          f"(mean |logit| {scale.mean():.4f}), clear-margin slots {clear.float().mean():.3f}, greedy tokens "
+          f"equal on {same.float().mean():.3f} of all slots", flush=True)
+    assert clear.float().mean() >= 0.85
+    assert same[clear].all()
 
 
 def test_spec_generate_is_lossless(dev):
