@@ -1676,8 +1676,15 @@ struct RowMerge {
 };
 
 // Adds the partials of row r of unit (b, ul) -- one per share its tiles fell to, in
-// slots unit + w -- each a normalized output with its LSE, values scaled by vs.
-template <int D>
+// slots unit + w -- each a normalized output with its LSE, values scaled by vs. The
+// segments go in batches of MB whose loads are all issued before any is used (one
+// memory round trip per batch: the loop's trip count is not known at compile time, so
+// the loads are gathered into registers explicitly), each batch merged relative to its
+// own largest LSE and then into the running merge. MB = 8 takes about three times the
+// registers of MB = 2 (121 against 42 VGPRs at D 128), which halves the combine's
+// occupancy: full batches (about two segments per unit) use 2, calls of few units
+// split over many shares 8.
+template <int D, int MB>
 __device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, int b, int ul, int r, int c,
                                                float vs, RowMerge &mg) {
   typedef __attribute__((ext_vector_type(2))) float f32x2_t;
@@ -1688,19 +1695,39 @@ __device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, 
   const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
   const int64_t nw = a.num_shares;
   const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
-  const int64_t wa = share_of(U0, total, nw), wb = share_of(U0 + tiles_b - 1, total, nw);
-  // The loads of different segments are independent.
-#pragma unroll 4
-  for (int64_t w = wa; w <= wb; ++w) {
-    const int64_t row = (unit + w) * rows + r;
-    const f32x2_t ls = *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row);
-    const u32x4_t ow = load16(a.part_o + row * D + 8 * c);
-    if (ls[0] == -INFINITY) continue;
-    f32x4_t x[2];
+  const int64_t wa = share_of(U0, total, nw);
+  const int nseg = (int)(share_of(U0 + tiles_b - 1, total, nw) - wa) + 1;
+  const int64_t row0 = (unit + wa) * rows + r;
+  for (int s0 = 0; s0 < nseg; s0 += MB) {
+    f32x2_t ls[MB];
+    u32x4_t ow[MB];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      x[j] = f32x4_t{f16_lo(ow[2 * j]), f16_hi(ow[2 * j]), f16_lo(ow[2 * j + 1]), f16_hi(ow[2 * j + 1])};
-    mg.add(ls[0], ls[1] * vs, 1.f, x);
+    for (int j = 0; j < MB; ++j) {
+      const int64_t row = row0 + (int64_t)(s0 + j) * rows;
+      const bool in = s0 + j < nseg;
+      ls[j] = in ? *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row) : f32x2_t{-INFINITY, 1.f};
+      ow[j] = in ? load16(a.part_o + row * D + 8 * c) : u32x4_t{0, 0, 0, 0};
+    }
+    float Mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) Mb = fmaxf(Mb, ls[j][0]);
+    if (Mb == -INFINITY) continue;  // no segment of the batch saw a position
+    f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    float den = 0.f;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const bool seen = ls[j][0] != -INFINITY;  // an empty segment adds nothing, whatever its values
+      const float f = seen ? __builtin_amdgcn_exp2f(ls[j][0] - Mb) : 0.f;
+      const float fx = f * (ls[j][1] * vs);
+      den += f;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const f32x4_t x = {f16_lo(ow[j][2 * k]), f16_hi(ow[j][2 * k]), f16_lo(ow[j][2 * k + 1]),
+                           f16_hi(ow[j][2 * k + 1])};
+        if (seen) acc[k] += x * fx;
+      }
+    }
+    mg.add(Mb, 1.f, den, acc);
   }
 }
 
@@ -1712,7 +1739,7 @@ __device__ __forceinline__ void store_row8(uint16_t *dst, const f32x4_t (&acc)[2
 // Merge each unit's partials and write the bf16 output; units of empty sequences get
 // zeros. One workgroup per 16-row block, one thread per (row, 8 channels), so the unit
 // and its sequence metadata are uniform per workgroup.
-template <int D>
+template <int D, int MB>
 __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
   constexpr int C = D / 8;  // 8-channel chunks per row
   const int rows = a.nrb * 16;
@@ -1728,7 +1755,7 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
   const int gq = R / a.q_len, tq = R - gq * a.q_len;
   if (gq >= a.group || tq >= qlen_b) return;
   RowMerge mg;
-  merge_partials<D>(a, unit, b, ul, r, c, a.vd ? a.v_scale * a.vd[(int64_t)b * a.d_sb + (int64_t)h * a.d_sh] : a.v_scale,
+  merge_partials<D, MB>(a, unit, b, ul, r, c, a.vd ? a.v_scale * a.vd[(int64_t)b * a.d_sb + (int64_t)h * a.d_sh] : a.v_scale,
                     mg);
   if (a.tail) {  // the verify tokens' partial
     typedef __attribute__((ext_vector_type(2))) float f32x2_t;
@@ -2092,13 +2119,20 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
                                           dim3(64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb)), kargs, 0, c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
-  // One workgroup of 2 D threads per 16-row block.
+  // One workgroup of 2 D threads per 16-row block; units split into many segments (a
+  // call of few units over the whole grid) merge their partials 8 at a time.
   const int64_t cblocks = units * sz.rp.nrb;
   FM_REQUIRE(cblocks < (1ll << 31), "too many units");
-  if (c.d == 128)
-    attn_combine_kernel<128><<<dim3((unsigned)cblocks), dim3(256), 0, c.stream>>>(a);
+  const bool many = units * 2 <= sz.num_shares;
+  const dim3 cg((unsigned)cblocks);
+  if (c.d == 128 && many)
+    attn_combine_kernel<128, 8><<<cg, dim3(256), 0, c.stream>>>(a);
+  else if (c.d == 128)
+    attn_combine_kernel<128, 2><<<cg, dim3(256), 0, c.stream>>>(a);
+  else if (many)
+    attn_combine_kernel<64, 8><<<cg, dim3(128), 0, c.stream>>>(a);
   else
-    attn_combine_kernel<64><<<dim3((unsigned)cblocks), dim3(128), 0, c.stream>>>(a);
+    attn_combine_kernel<64, 2><<<cg, dim3(128), 0, c.stream>>>(a);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
