@@ -101,7 +101,8 @@ SIGNATURES: dict[str, tuple] = {
     "fm_argmax_rows": (c_int, [P, I32, I64, I64, I64, P, P, c_size_t, P]),
     "fm_sample_rows": (c_int, [P, I32, I64, I64, I64, P, P, P, P, P, c_size_t, P]),
     "fm_seeded_normal": (c_int, [P, P, I32, P, I32, I64, I64, F32, P, I64, P]),
-    "fm_adaln_residual": (c_int, [P, I64, P, I64, P, P, P, P, I64, P, I64, I64, I32, F32, P]),
+    "fm_adaln_residual": (c_int, [P, I64, P, I64, P, I32, P, P, P, I64, P, I64, I64, I32, F32, P]),
+    "fm_noise_rows": (c_int, [P, I64, I32, I64, P, F32, F32, P, I64, P, P]),
     "fm_profile_enable": (c_int, [c_int]),
     "fm_profile_read": (c_int, [ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]),
 }

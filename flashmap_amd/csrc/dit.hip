@@ -15,7 +15,13 @@
 // Layout: rows of `dim` bf16 values with a row stride, one wavefront per row; lane l
 // holds the 16-byte chunks l, l + 64, ... of its row (coalesced 1 KiB per wavefront
 // load). gate, scale and shift are (dim,) vectors shared by every row: the modulations
-// depend on the jump's times only.
+// depend on the jump's times only. Two variants serve the folded noise read-out of a
+// one-jump draft (flashmap/vllm/model.py:915-925): the gate one bf16 scalar per row, and
+// x one (dim,) row shared by all rows (row stride 0).
+//
+// fm_noise_rows, that read-out's row pass: per row of the fp32 noise z (H values) the
+// scale bf16(gain * rsqrt(sum_i z_i^2 lambda_i + eps)) and z rounded to bf16 for the
+// folded GEMM; one wavefront per row, 16-byte loads.
 #include "fm_device.h"
 #include "fm_host.h"
 
@@ -25,6 +31,7 @@ struct AdalnArgs {
   const uint16_t *x;
   const uint16_t *y;  // NULL: no residual, x' = x
   const uint16_t *gate, *scale, *shift;  // scale NULL: no norm
+  int32_t gate_rows;  // nonzero: gate holds one value per row
   uint16_t *x_out;  // NULL: x' not stored
   uint16_t *h_out;
   int64_t rows;
@@ -54,7 +61,14 @@ __global__ __launch_bounds__(256) void adaln_residual_kernel(const AdalnArgs a) 
       const u32x4_t xv = load16(a.x + row * a.xs + 8 * c);
       if (a.y != nullptr) {
         const u32x4_t yv = load16(a.y + row * a.ys + 8 * c);
-        const u32x4_t gv = load16(a.gate + 8 * c);
+        u32x4_t gv;
+        if (a.gate_rows) {
+          const uint32_t gr = a.gate[row];
+          const uint32_t g2 = gr | (gr << 16);
+          gv = u32x4_t{g2, g2, g2, g2};
+        } else {
+          gv = load16(a.gate + 8 * c);
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float lo = __fadd_rn(bf16_lo(xv[q]), round_bf16(__fmul_rn(bf16_lo(gv[q]), bf16_lo(yv[q]))));
@@ -109,14 +123,44 @@ __global__ __launch_bounds__(256) void adaln_residual_kernel(const AdalnArgs a) 
   }
 }
 
+// One wavefront per row of z (fp32, H values): lane l holds the 4-value chunks l, l + 64, ...
+template <int NCH>
+__global__ __launch_bounds__(256) void noise_rows_kernel(const float *__restrict__ z, int64_t rows, int32_t h,
+                                                         int64_t zs, const float *__restrict__ lam, float eps,
+                                                         float gain, uint16_t *__restrict__ z16, int64_t z16s,
+                                                         uint16_t *__restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= rows) return;  // wave-uniform
+  const int chunks = h >> 2;
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = lane + 64 * i;
+    if (c < chunks) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t *>(z + row * zs + 4 * c);
+      const f32x4_t l = *reinterpret_cast<const f32x4_t *>(lam + 4 * c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = __builtin_fmaf(__fmul_rn(v[q], v[q]), l[q], acc);
+      *reinterpret_cast<u32x2_t *>(z16 + row * z16s + 4 * c) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, m, 64));
+  if (lane == 0) {
+    const float s = __fmul_rn(gain, rsqrtf(__fadd_rn(acc, eps)));
+    scale[row] = (uint16_t)(pack_bf16x2(s, 0.f) & 0xffffu);
+  }
+}
+
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace fm
 
 extern "C" int fm_adaln_residual(const void *x, int64_t x_stride, const void *y, int64_t y_stride,
-                                 const void *gate, const void *scale, const void *shift, void *x_out,
-                                 int64_t x_out_stride, void *h_out, int64_t h_out_stride, int64_t rows,
-                                 int32_t dim, float eps, void *stream) {
+                                 const void *gate, int32_t gate_per_row, const void *scale, const void *shift,
+                                 void *x_out, int64_t x_out_stride, void *h_out, int64_t h_out_stride,
+                                 int64_t rows, int32_t dim, float eps, void *stream) {
   using namespace fm;
   FM_REQUIRE(rows >= 0 && dim > 0, "bad sizes: rows=%lld dim=%d", (long long)rows, dim);
   if (rows == 0) return FM_OK;
@@ -130,14 +174,17 @@ extern "C" int fm_adaln_residual(const void *x, int64_t x_stride, const void *y,
   for (const void *p : ptrs) FM_REQUIRE(p == nullptr || aligned16(p), "tensors must be 16-byte aligned");
   FM_REQUIRE(x_stride % 8 == 0 && y_stride % 8 == 0 && x_out_stride % 8 == 0 && h_out_stride % 8 == 0,
              "row strides must be multiples of 8 elements");
-  FM_REQUIRE(x_stride >= dim && (y == nullptr || y_stride >= dim) && (x_out == nullptr || x_out_stride >= dim) &&
-                 (h_out == nullptr || h_out_stride >= dim),
-             "row strides must cover a row of %d", dim);
+  FM_REQUIRE((x_stride == 0 || x_stride >= dim) && (y == nullptr || y_stride >= dim) &&
+                 (x_out == nullptr || x_out_stride >= dim) && (h_out == nullptr || h_out_stride >= dim),
+             "row strides must cover a row of %d (x may also be one shared row, stride 0)", dim);
+  FM_REQUIRE(x_stride != 0 || x_out != x, "a shared x row cannot be written in place");
   const int64_t blocks = (rows + 3) / 4;
   FM_REQUIRE(blocks < (1ll << 31), "too many rows");
-  AdalnArgs a{(const uint16_t *)x, (const uint16_t *)y, (const uint16_t *)gate, (const uint16_t *)scale,
-              (const uint16_t *)shift, (uint16_t *)x_out, (uint16_t *)h_out, rows, x_stride, y_stride,
-              x_out_stride, h_out_stride, dim, eps};
+  AdalnArgs a{(const uint16_t *)x,     (const uint16_t *)y,     (const uint16_t *)gate,
+              (const uint16_t *)scale, (const uint16_t *)shift, gate_per_row,
+              (uint16_t *)x_out,       (uint16_t *)h_out,       rows,
+              x_stride,                y_stride,                x_out_stride,
+              h_out_stride,            dim,                     eps};
   hipStream_t s = (hipStream_t)stream;
   const int per_lane = (dim / 8 + 63) / 64;
   const dim3 grid((unsigned)blocks), block(256);
@@ -151,6 +198,35 @@ extern "C" int fm_adaln_residual(const void *x, int64_t x_stride, const void *y,
     adaln_residual_kernel<8><<<grid, block, 0, s>>>(a);
   else
     adaln_residual_kernel<16><<<grid, block, 0, s>>>(a);
+  FM_CHECK_HIP(hipGetLastError());
+  return FM_OK;
+}
+
+extern "C" int fm_noise_rows(const float *z, int64_t rows, int32_t hidden, int64_t z_stride, const float *eigvals,
+                             float eps, float gain, void *z_bf16, int64_t z_bf16_stride, void *scale,
+                             void *stream) {
+  using namespace fm;
+  FM_REQUIRE(rows >= 0 && hidden > 0, "bad sizes: rows=%lld hidden=%d", (long long)rows, hidden);
+  if (rows == 0) return FM_OK;
+  if (hidden % 4 != 0 || hidden > 16384)
+    return fail(FM_ERR_UNSUPPORTED, "hidden %d not supported (a multiple of 4, at most 16384)", hidden);
+  FM_REQUIRE(z && eigvals && z_bf16 && scale, "NULL tensor pointer");
+  FM_REQUIRE(aligned16(z) && aligned16(eigvals) && ((uintptr_t)z_bf16 & 7) == 0,
+             "z / eigvals must be 16-byte aligned, z_bf16 8-byte aligned");
+  FM_REQUIRE(z_stride % 4 == 0 && z_stride >= hidden && z_bf16_stride % 4 == 0 && z_bf16_stride >= hidden,
+             "row strides must be multiples of 4 covering a row");
+  const int64_t blocks = (rows + 3) / 4;
+  FM_REQUIRE(blocks < (1ll << 31), "too many rows");
+  hipStream_t s = (hipStream_t)stream;
+  const int per_lane = (hidden / 4 + 63) / 64;
+  const dim3 grid((unsigned)blocks), block(256);
+  uint16_t *zo = (uint16_t *)z_bf16, *so = (uint16_t *)scale;
+  if (per_lane <= 8)
+    noise_rows_kernel<8><<<grid, block, 0, s>>>(z, rows, hidden, z_stride, eigvals, eps, gain, zo, z_bf16_stride, so);
+  else if (per_lane <= 16)
+    noise_rows_kernel<16><<<grid, block, 0, s>>>(z, rows, hidden, z_stride, eigvals, eps, gain, zo, z_bf16_stride, so);
+  else
+    noise_rows_kernel<64><<<grid, block, 0, s>>>(z, rows, hidden, z_stride, eigvals, eps, gain, zo, z_bf16_stride, so);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }

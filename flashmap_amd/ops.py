@@ -21,6 +21,7 @@ from ._native import call
 __all__ = [
     "Rope",
     "adaln_residual",
+    "noise_rows",
     "argmax_rows",
     "attention_plan",
     "block_attention_contig",
@@ -1148,48 +1149,75 @@ def adaln_residual(
     modulation: tuple[torch.Tensor, torch.Tensor] | None,
     eps: float,
     x_out: torch.Tensor | None = None,
+    gate_per_row: bool = False,
 ) -> tuple[torch.Tensor | None, torch.Tensor | None]:
     """The DiT's residual stream in one pass: ``x' = x + gate * y`` (skipped when ``y``
     is None), then ``h = LN(x') * (1 + scale) + shift`` for ``modulation = (scale,
     shift)`` (skipped when None), each op rounded to bf16 like torch's eager ops
-    (flashmap/modeling_flashmap.py:114-117, 185-192). ``x``/``y (..., dim)`` bf16;
-    ``gate``, ``scale``, ``shift``: ``dim`` values shared by every row. ``x_out`` (may
-    be ``x``) receives ``x'``, else a new tensor does. Returns ``(x', h)``, ``x'`` None
-    without a residual."""
+    (flashmap/modeling_flashmap.py:114-117, 185-192). ``x``/``y (..., dim)`` bf16, or
+    ``x (dim,)``: one row shared by every row of ``y``; ``gate``, ``scale``, ``shift``:
+    ``dim`` values shared by every row (``gate_per_row``: one gate value per row).
+    ``x_out`` (may be ``x``) receives ``x'``, else a new tensor does. Returns ``(x',
+    h)``, ``x'`` None without a residual."""
     _check_cuda(x, y, gate, x_out, *(modulation or ()))
     dim = x.shape[-1]
     if dim % 8 or not 0 < dim <= 8192:
         raise ValueError(f"rows of {dim} values: the kernel takes a multiple of 8, at most 8192")
-    xr = _rows2d(x, dim, "x")
-    rows = xr.shape[0]
+    shared = x.dim() == 1 and y is not None
+    shape = y.shape if shared else x.shape
+    xr = _vec(x, dim, "x")[None] if shared else _rows2d(x, dim, "x")
+    x_stride = 0 if shared else xr.stride(0)
+    rows = math.prod(shape[:-1])
     yr = g = xo = None
     if y is not None:
         if gate is None:
             raise ValueError("a residual needs its gate")
-        if y.numel() != x.numel():
-            raise ValueError(f"y holds {y.numel()} values, x {x.numel()}")
-        yr, g = _rows2d(y, dim, "y"), _vec(gate, dim, "gate")
+        if y.shape[-1] != dim or (not shared and y.numel() != x.numel()):
+            raise ValueError(f"y {tuple(y.shape)} does not match x {tuple(x.shape)}")
+        yr = _rows2d(y, dim, "y")
+        g = _vec(gate, rows, "gate (one per row)") if gate_per_row else _vec(gate, dim, "gate")
         if x_out is None:
-            x_out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
-        if x_out.numel() != x.numel():
-            raise ValueError(f"x_out holds {x_out.numel()} values, x {x.numel()}")
+            x_out = torch.empty(shape, dtype=torch.bfloat16, device=x.device)
+        if x_out.numel() != rows * dim:
+            raise ValueError(f"x_out holds {x_out.numel()} values, the stream {rows * dim}")
         xo = x_out.view(rows, dim)  # raises unless x_out's rows are one strided view
         if xo.stride(-1) != 1 or xo.stride(0) % 8 or xo.data_ptr() % 16:
             raise ValueError("x_out must hold 16-byte aligned rows with unit channel stride")
     h = sc = sh = None
     if modulation is not None:
         sc, sh = (_vec(m, dim, n) for m, n in zip(modulation, ("scale", "shift")))
-        h = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+        h = torch.empty(shape, dtype=torch.bfloat16, device=x.device)
     if rows == 0 or (yr is None and h is None):
         return x_out, h
     hr = None if h is None else h.view(rows, dim)
     call(
         "fm_adaln_residual",
-        xr.data_ptr(), xr.stride(0), _ptr(yr), 0 if yr is None else yr.stride(0), _ptr(g), _ptr(sc), _ptr(sh),
-        _ptr(xo), 0 if xo is None else xo.stride(0), _ptr(hr), 0 if hr is None else hr.stride(0),
-        rows, dim, float(eps), _stream(x),
+        xr.data_ptr(), x_stride, _ptr(yr), 0 if yr is None else yr.stride(0), _ptr(g), int(gate_per_row),
+        _ptr(sc), _ptr(sh), _ptr(xo), 0 if xo is None else xo.stride(0), _ptr(hr), 0 if hr is None else hr.stride(0),
+        rows, dim, float(eps), _stream(y if shared else x),
     )
     return x_out, h
+
+
+def noise_rows(z: torch.Tensor, eigvals: torch.Tensor, eps: float, gain: float,
+               z_bf16: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The folded noise read-out's row pass (flashmap/vllm/model.py:915-925): for ``z
+    (rows, H)`` float32, ``(z in bf16, bf16(gain * rsqrt(z^2 @ eigvals + eps)) (rows,))``."""
+    _check_cuda(z, eigvals, z_bf16)
+    if z.dtype != torch.float32 or z.dim() != 2 or z.stride(-1) != 1:
+        raise ValueError("z must be float32 (rows, H) with unit channel stride")
+    rows, hidden = z.shape
+    if z.stride(0) % 4 or z.data_ptr() % 16:
+        z = z.contiguous()
+    lam = _f32(eigvals)
+    _need_numel(lam, hidden, "eigvals")
+    if z_bf16 is None:
+        z_bf16 = torch.empty(rows, hidden, dtype=torch.bfloat16, device=z.device)
+    scale = torch.empty(rows, dtype=torch.bfloat16, device=z.device)
+    if rows:
+        call("fm_noise_rows", z.data_ptr(), rows, hidden, z.stride(0), lam.data_ptr(), float(eps), float(gain),
+             z_bf16.data_ptr(), z_bf16.stride(0), scale.data_ptr(), _stream(z))
+    return z_bf16, scale
 
 
 def default_scale(head_dim: int) -> float:

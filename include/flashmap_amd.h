@@ -410,18 +410,32 @@ int fm_seeded_normal(const int64_t *seeds, const void *rows, int32_t rows_int64,
 /* ---------------------------------------------------------------------------------
  * f3: the DiT's residual stream between sublayers. Replaces the eager ops of
  * FlashMapAdaLayerNorm.forward and the gated residuals of FlashMapLayer.forward
- * (flashmap/modeling_flashmap.py:114-117, 185-192):
+ * (flashmap/modeling_flashmap.py:114-117, 185-192) and of the vLLM draft step's _dit
+ * (flashmap/vllm/model.py:829-903):
  *   x' = x + gate * y                          (when y is non-NULL; else x' = x)
  *   h  = LN(x') * (1 + scale) + shift          (when scale is non-NULL)
  * with every op rounded to bf16 as torch's eager bf16 ops round; LN has no affine
  * weights (biased variance, eps inside the rsqrt). x, y, x_out, h_out: (rows, dim) bf16
- * with row strides (elements, multiples of 8); gate, scale, shift: (dim,) bf16 shared by
- * all rows; x_out may alias x. dim a multiple of 8, at most 8192.
+ * with row strides (elements, multiples of 8); x_stride 0 reads one (dim,) row for every
+ * row; scale, shift: (dim,) bf16 shared by all rows; gate: (dim,) bf16 shared by all
+ * rows, or with gate_per_row nonzero one bf16 value per row (rows,); x_out may alias x
+ * (not a shared x row). dim a multiple of 8, at most 8192.
  */
 int fm_adaln_residual(const void *x, int64_t x_stride, const void *y, int64_t y_stride,
-                      const void *gate, const void *scale, const void *shift, void *x_out,
-                      int64_t x_out_stride, void *h_out, int64_t h_out_stride, int64_t rows,
-                      int32_t dim, float eps, void *stream);
+                      const void *gate, int32_t gate_per_row, const void *scale, const void *shift,
+                      void *x_out, int64_t x_out_stride, void *h_out, int64_t h_out_stride,
+                      int64_t rows, int32_t dim, float eps, void *stream);
+
+/* The row pass of the one-jump draft's folded noise read-out (flashmap/vllm/model.py:
+ * 915-925 with the folds of flashmap/vllm/fold.py:45-75): for z (rows, hidden) fp32 with a
+ * row stride, scale[r] = bf16(gain * rsqrt(sum_i z[r,i]^2 eigvals[i] + eps)) (bf16, rows)
+ * and z_bf16 = z rounded to bf16 (the folded GEMM's operand). The read-out is then
+ * noise = z_bf16 @ M^T and hidden = first_hidden + scale * noise (fm_adaln_residual with
+ * a shared x row and a per-row gate). hidden a multiple of 4, at most 16384.
+ */
+int fm_noise_rows(const float *z, int64_t rows, int32_t hidden, int64_t z_stride,
+                  const float *eigvals, float eps, float gain, void *z_bf16,
+                  int64_t z_bf16_stride, void *scale, void *stream);
 
 /* ---------------------------------------------------------------------------------
  * Measurement hook. No reference counterpart: it lets a benchmark time the main

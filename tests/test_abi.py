@@ -97,17 +97,23 @@ def test_residual_stream_argument_errors(lib):
 
     x = ctypes.c_void_p(16)
     f = ctypes.c_float(1e-6)
-    rc = lib.fm_adaln_residual(x, 16, x, 16, x, x, x, x, 16, x, 16, 4, 12, f, None)
+    rc = lib.fm_adaln_residual(x, 16, x, 16, x, 0, x, x, x, 16, x, 16, 4, 12, f, None)
     assert rc == n.FM_ERR_UNSUPPORTED and "dim 12" in _err(lib)
-    rc = lib.fm_adaln_residual(x, 16384, x, 16384, x, x, x, x, 16384, x, 16384, 4, 16384, f, None)
+    rc = lib.fm_adaln_residual(x, 16384, x, 16384, x, 0, x, x, x, 16384, x, 16384, 4, 16384, f, None)
     assert rc == n.FM_ERR_UNSUPPORTED and "at most 8192" in _err(lib)
-    rc = lib.fm_adaln_residual(x, 64, x, 64, None, x, x, x, 64, x, 64, 4, 64, f, None)
+    rc = lib.fm_adaln_residual(x, 64, x, 64, None, 0, x, x, x, 64, x, 64, 4, 64, f, None)
     assert rc == n.FM_ERR_INVALID and "gate" in _err(lib)
-    rc = lib.fm_adaln_residual(x, 64, None, 0, None, None, None, None, 0, None, 0, 4, 64, f, None)
+    rc = lib.fm_adaln_residual(x, 64, None, 0, None, 0, None, None, None, 0, None, 0, 4, 64, f, None)
     assert rc == n.FM_ERR_INVALID and "nothing to write" in _err(lib)
-    rc = lib.fm_adaln_residual(x, 60, None, 0, None, x, x, None, 0, x, 64, 4, 64, f, None)
+    rc = lib.fm_adaln_residual(x, 60, None, 0, None, 0, x, x, None, 0, x, 64, 4, 64, f, None)
     assert rc == n.FM_ERR_INVALID and "multiples of 8" in _err(lib)
-    assert lib.fm_adaln_residual(None, 0, None, 0, None, None, None, None, 0, None, 0, 0, 64, f, None) == n.FM_OK
+    rc = lib.fm_adaln_residual(x, 0, x, 64, x, 1, x, x, x, 64, x, 64, 4, 64, f, None)
+    assert rc == n.FM_ERR_INVALID and "shared x row" in _err(lib)
+    assert lib.fm_adaln_residual(None, 0, None, 0, None, 0, None, None, None, 0, None, 0, 0, 64, f, None) == n.FM_OK
+    rc = lib.fm_noise_rows(x, 4, 30, 32, x, f, f, x, 32, x, None)
+    assert rc == n.FM_ERR_UNSUPPORTED and "hidden 30" in _err(lib)
+    rc = lib.fm_noise_rows(x, 4, 32, 30, x, f, f, x, 32, x, None)
+    assert rc == n.FM_ERR_INVALID and "row strides" in _err(lib)
 
 
 def test_plan_and_workspace_sizes_without_device(lib):
