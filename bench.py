@@ -316,6 +316,149 @@ def _flushed(call, args, dev, flush_mb: int = 512) -> dict:
             "kernel_ms": tot.value / max(cnt.value, 1)}
 
 
+# The vLLM plugin's one-jump draft step (flashmap_amd.draft_step.DraftStep): name ->
+# (requests, ctx lo, ctx hi, drafter config overrides). The released 8B drafter's shape
+# (hidden 2048, 16 heads of 128, 6 layers, GELU MLP 8192) over a Qwen3-8B target (hidden
+# 4096, vocabulary 151936); contexts drawn as C3's, paged in 16-token blocks.
+DRAFT_STEP_WORKLOADS = {
+    "draft-step-8b-b64": (64, 256, 8192, {}),
+}
+
+
+def _draft_weights(step) -> dict:
+    """The oracle's plain-tensor view of a prepared DraftStep (on the CPU)."""
+    m, cpu = step.model, (lambda t: t.detach().cpu())
+    w = {"embed": cpu(step.embed_weight), "anchor_proj.weight": cpu(m.anchor_proj.weight),
+         "anchor_proj.bias": cpu(m.anchor_proj.bias), "anchor_norm.weight": cpu(m.anchor_norm.weight),
+         "anchor_norm.eps": m.anchor_norm.eps, "context_kv_weight": cpu(step.context_kv_weight),
+         "context_k_norm": cpu(step.context_k_norm), "k_eps": step.k_eps, "cos_sin": cpu(step.cos_sin),
+         "heads": step.heads, "block": step.block, "noise_eigvals": cpu(step.noise_eigvals),
+         "noise_embed": cpu(step.noise_embed), "noise_eps": step.noise_eps, "gain": step.noise_gain,
+         "first_hidden": cpu(step.first_hidden), "ln_eps": m.final_adaln.eps,
+         "final_mod": [cpu(t) for t in step.final_mod], "head_weight": cpu(step.head_weight),
+         "head_bias": cpu(step.head_bias), "layers": []}
+    for i, layer in enumerate(m.layers):
+        lw = {"mods": [[cpu(t) for t in mod] for mod in step.layer_mods[i]], "self_qkv": cpu(step.self_qkv[i]),
+              "self_q_norm": cpu(layer.self_attn.q_norm.weight), "self_k_norm": cpu(layer.self_attn.k_norm.weight),
+              "qk_eps": layer.self_attn.q_norm.eps, "self_o": cpu(layer.self_attn.o_proj.weight),
+              "cross_q": cpu(layer.cross_attn.q_proj.weight), "cross_q_norm": cpu(layer.cross_attn.q_norm.weight),
+              "cross_o": cpu(layer.cross_attn.o_proj.weight)}
+        lw.update({k: cpu(v) for k, v in layer.mlp.state_dict().items()})
+        w["layers"].append(lw)
+    return w
+
+
+def run_draft_step(args, dev) -> dict:
+    """One call = one draft step for the batch: the anchors' context rows written, the
+    folded noise read-out, 6 DiT layers (each with its cross-attention over its paged
+    cache), the folded head over the vocabulary and the greedy argmax. The plan is built
+    per step inside the call."""
+    from flashmap_amd import drafter as d
+    from flashmap_amd.draft_step import DraftStep
+
+    batch, lo, hi, over = DRAFT_STEP_WORKLOADS[args.workload]
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(lo, hi + 1, (batch,), generator=g)  # C3's draw: context positions incl. the anchor
+    page = 16
+    pages = [math.ceil(int(n) / page) for n in lens]
+    total = sum(pages)
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros(batch, max(pages), dtype=torch.int32)
+    o = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[o:o + n].int()
+        o += n
+    torch.manual_seed(0)
+    model = d.FlashMapDraftModel(d.drafter_config(**over)).to(dev, torch.bfloat16)
+    cfg = model.config
+    gd = torch.Generator(device=dev).manual_seed(0)
+    embed = torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=gd, device=dev).bfloat16()
+    lm_head = (torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=gd, device=dev) / 64).bfloat16()
+    step = DraftStep(model, embed, lm_head, max_model_len=hi + cfg.block_size + 1)
+    heads, hd = step.heads, step.head_dim
+    caches = []
+    for _ in model.layers:
+        c = torch.empty(total, heads, page, 2 * hd, dtype=torch.bfloat16, device=dev)
+        c.normal_(generator=gd)
+        caches.append(c)
+    layout = step.cache_layout(caches)
+    anchors = torch.randint(0, cfg.vocab_size, (batch,), generator=g).to(dev)
+    a_pos = (lens - 1).to(dev)
+    a_slots = (bt[torch.arange(batch), (lens - 1) // page].long() * page + (lens - 1) % page).to(dev)
+    z = torch.randn(batch * cfg.block_size, cfg.target_hidden_size, generator=gd, device=dev)
+    bt_d = bt.to(dev)
+    tokens = torch.empty(batch * cfg.block_size, dtype=torch.int64, device=dev)
+
+    def call():
+        tokens.copy_(step.greedy(step(anchors, a_pos, a_slots, z, caches, bt_d, layout)))
+
+    timing = _measure(call, args)
+    ms, kernel_ms = timing["ms"], timing["kernel_ms"]
+    sum_l = int(lens.sum())
+    k_rows, layers = cfg.block_size, len(model.layers)
+    attn_bytes = sum_l * heads * hd * 2 * 2 + 2 * batch * k_rows * heads * hd * 2 + 4 * total + 8 * batch \
+        + batch * k_rows * hd * 4
+    gbs = attn_bytes / (kernel_ms * 1e-3) / 1e9
+    dim, inter, th, vocab = cfg.hidden_size, cfg.intermediate_size, cfg.target_hidden_size, cfg.vocab_size
+    rows = batch * k_rows
+    gemm_flops = 2 * rows * (layers * (3 * dim * dim + 3 * dim * dim + 2 * dim * inter) + vocab * dim + th * dim) \
+        + 2 * batch * (th * dim + 2 * layers * dim * dim)
+    result = {
+        "metric": "one-jump draft step µs/step (anchor write, noise read-out, 6 DiT layers, folded head, argmax), "
+                  "8B drafter, K=16, batch 64, ctx 256–8k, 1 GPU",
+        "value": round(ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: random-init drafter and target embedding / LM head, random paged K/V, "
+                                 "seeded draw of lengths and block table (C3's)",
+        "config": {"workload": args.workload, "batch": batch, "hidden": dim, "heads": heads, "head_dim": hd,
+                   "layers": layers, "intermediate": inter, "mlp": cfg.mlp_type, "vocab": vocab,
+                   "target_hidden": th, "block_queries": k_rows, "ctx_lo": lo, "ctx_hi": hi, "ctx_sum": sum_l,
+                   "page": page},
+        "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel (the step's cross-attention, one launch per layer)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": attn_bytes,
+                     "kernel_us": round(kernel_ms * 1e3, 2)},
+        "attention_share": round(layers * kernel_ms / ms, 4),
+        "gemm_tflop_per_step": round(gemm_flops / 1e12, 4),
+        **_timing_fields(timing),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = draft_step_cpu_baseline(step, lens, anchors.cpu(), z.cpu(), args.cpu_budget)
+    return result
+
+
+def draft_step_cpu_baseline(step, lens, anchors, z, budget_s) -> dict:
+    """The draft-step oracle (fp32/bf16 torch on the host cores) request by request, each
+    over a CPU paged cache of its own context (random values: the time does not depend on
+    them), until the budget is spent; scaled to the batch by requests."""
+    from oracle import draft_step as oracle
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = _draft_weights(step)
+    k, page = step.block, 16
+    g = torch.Generator().manual_seed(1)
+    done, t_used = 0, 0.0
+    for b in range(len(lens)):
+        n = int(lens[b])
+        blocks = math.ceil(n / page)
+        caches = [torch.randn(blocks, step.heads, page, 2 * step.head_dim, generator=g).bfloat16()
+                  for _ in step.model.layers]
+        bt = torch.arange(blocks, dtype=torch.int32)[None]
+        pos = torch.tensor([n - 1])
+        t0 = time.perf_counter()
+        oracle.write_anchor_rows(w, anchors[b:b + 1], pos, pos.clone(), caches, page)
+        hidden = oracle.one_jump(w, anchors[b:b + 1], pos, z[b * k:(b + 1) * k], caches, bt)
+        oracle.draft_logits(w, hidden).argmax(-1)
+        t_used += time.perf_counter() - t0
+        done += 1
+        if t_used > budget_s:
+            break
+    return {"value": round(t_used / done * len(lens) * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
+            "sample": f"first {done} of {len(lens)} requests: the oracle's anchor write, read-out, DiT and folded "
+                      "head + argmax, scaled by requests"}
+
+
 # The batch-1 contiguous case (FlashMapCache views): name -> (batch, hq, hkv, head_dim, K,
 # context positions). Keys are drawn as already normed and rotated (the cache's state).
 CONTIG_WORKLOADS = {
@@ -439,6 +582,54 @@ def _measure(call, args, kernel_events: bool = True) -> dict:
         kernel_ms = tot.value / max(cnt.value, 1)
     return {"ms": ms, "kernel_ms": kernel_ms, "cold_ms": cold,
             "settle": {"ms": round(settle_ms, 1), "calls": settle_calls}}
+
+
+def drift_series(call, calls: int, dev, copy_every: int = 250) -> dict:
+    """The call back to back from an idle GPU: each call's duration (events around it), the
+    shader clock right after it (fm_clock_probe: shader-clock ticks over 100 MHz real-time
+    ticks across a 4000-tick spin), and a 1 GiB copy every ``copy_every`` calls as a
+    bandwidth control. Summaries per 50 calls, the first 40 calls in full."""
+    import ctypes
+
+    from flashmap_amd import _native
+
+    probes = torch.zeros(calls, 2, dtype=torch.int64, device=dev)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream().cuda_stream
+    call()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    time.sleep(0.5)  # idle, as after set-up
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * calls)]
+    copies = []
+    for i in range(calls):
+        ev[2 * i].record()
+        call()
+        ev[2 * i + 1].record()
+        _native.call("fm_clock_probe", ctypes.c_void_p(probes[i].data_ptr()), ctypes.c_uint64(4000),
+                     ctypes.c_void_p(stream))
+        if copy_every and (i + 1) % copy_every == 0:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            dst.copy_(src)
+            b.record()
+            copies.append((i + 1, a, b))
+    torch.cuda.synchronize()
+    us = [ev[2 * i].elapsed_time(ev[2 * i + 1]) * 1e3 for i in range(calls)]
+    p = probes.cpu().double()
+    ghz = (p[:, 0] / (p[:, 1] / 100e6) / 1e9).tolist()
+    start = [ev[0].elapsed_time(ev[2 * i]) for i in range(calls)]
+    med = lambda xs: sorted(xs)[len(xs) // 2]  # noqa: E731
+    return {
+        "workload": "c3-qwen3-8b-paged-b64", "calls": calls,
+        "first_40": [{"ms_since_start": round(start[i], 2), "us": round(us[i], 1), "sclk_ghz": round(ghz[i], 2)}
+                     for i in range(min(40, calls))],
+        "per_50": [{"calls": f"{s}-{min(calls, s + 50) - 1}", "median_us": round(med(us[s:s + 50]), 1),
+                    "median_sclk_ghz": round(med(ghz[s:s + 50]), 2)} for s in range(0, calls, 50)],
+        "copy_1gib": [{"after_call": i, "tbs": round(2 * (1 << 30) / (a.elapsed_time(b) * 1e-3) / 1e12, 3)}
+                      for i, a, b in copies],
+    }
 
 
 def _timing_fields(t: dict) -> dict:
@@ -636,11 +827,14 @@ def main() -> int:
     ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64",
                     choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS)
                     + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS) + sorted(SELECT_WORKLOADS)
-                    + sorted(CONTIG_WORKLOADS))
+                    + sorted(CONTIG_WORKLOADS) + sorted(DRAFT_STEP_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--settle-ms", type=float, default=100.0,
                     help="back-to-back calls before the timed ones (the GPU's clocks settle under the load)")
+    ap.add_argument("--drift", type=int, default=0,
+                    help="only print the per-call duration and shader-clock series of N calls of the C3 call "
+                         "from an idle GPU")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="only run N copies of a 1 GiB buffer (HBM counter calibration)")
     args = ap.parse_args()
@@ -669,6 +863,9 @@ def main() -> int:
         return 0
     if args.workload in CONTIG_WORKLOADS:
         print(json.dumps(run_contig(args, dev)))
+        return 0
+    if args.workload in DRAFT_STEP_WORKLOADS:
+        print(json.dumps(run_draft_step(args, dev)))
         return 0
 
     from flashmap_amd import _native, ops
@@ -726,6 +923,9 @@ def main() -> int:
             ops.block_attention_paged(q_pre, cache, cu, lens, bt, k_rows, max_k, d ** -0.5,
                                       prologue=pro, plan=plan, out=out)
 
+    if args.drift:
+        print(json.dumps(drift_series(call, args.drift, dev)))
+        return 0
     ms, kernel_ms, timing = _time_call(call, args)
 
     ab = algorithmic_bytes(inp, kv_bytes=1 if fp8 else 2)

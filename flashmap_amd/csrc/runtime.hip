@@ -77,6 +77,22 @@ void profile_after(hipStream_t stream) {
   g_prof.pending.back().second = b;
 }
 
+// Measurement hook: one wavefront reads the shader-clock counter (s_memtime) and the
+// 100 MHz real-time counter (s_memrealtime), spins until `spin` shader-clock ticks have
+// passed (a bounded loop: the counter only grows) and stores both elapsed counts with a
+// vector store, so (ticks / (real ticks / 100 MHz)) is the shader clock of that moment.
+__global__ __launch_bounds__(64) void clock_probe_kernel(uint64_t *out, uint64_t spin) {
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  uint64_t t = t0;
+  while (t - t0 < spin) t = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    out[0] = t - t0;
+    out[1] = r1 - r0;
+  }
+}
+
 }  // namespace fm
 
 extern "C" {
@@ -94,6 +110,14 @@ int fm_device_cus(int device, int *num_cus) {
 int fm_profile_enable(int enable) {
   std::lock_guard<std::mutex> lock(fm::g_prof.mu);
   fm::g_prof.enabled = enable != 0;
+  return FM_OK;
+}
+
+int fm_clock_probe(uint64_t *out, uint64_t spin_ticks, void *stream) {
+  FM_REQUIRE(out != nullptr && ((uintptr_t)out & 15) == 0, "out must be a 16-byte aligned device pointer");
+  FM_REQUIRE(spin_ticks > 0 && spin_ticks <= (1ull << 24), "spin_ticks must lie in (0, 2^24]");
+  fm::clock_probe_kernel<<<1, 64, 0, (hipStream_t)stream>>>(out, spin_ticks);
+  FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
 

@@ -84,6 +84,9 @@ class DraftStep:
         self.k_eps = layers[0].cross_attn.k_norm.eps if len(layers) else 0.0
         self.self_qkv = [torch.cat([l.self_attn.q_proj.weight, l.self_attn.k_proj.weight, l.self_attn.v_proj.weight])
                          for l in layers]
+        # the kernels read the q/k norm weights as float32: converted once here, not per call
+        self.norms = [tuple(n.weight.float().contiguous() for n in (l.self_attn.q_norm, l.self_attn.k_norm,
+                                                                     l.cross_attn.q_norm)) for l in layers]
         self.cos_sin = _rope_table(max_model_len + self.block + 1, self.head_dim, cfg.rope_theta,
                                    state_embed.device)
         self.rope = ops.rope_from_table(self.cos_sin)
@@ -149,15 +152,14 @@ class DraftStep:
         heads, hd, tokens = self.heads, self.head_dim, batch * k
         for i, layer in enumerate(model.layers):
             (_, _, g_self), (c_scale, c_shift, g_cross), (m_scale, m_shift, g_mlp) = mods[i]
+            self_qn, self_kn, cross_qn = self.norms[i]
             attn = ops.block_self_attention(F.linear(h, self.self_qkv[i]).view(batch, k, 3, heads, hd),
-                                            layer.self_attn.q_norm.weight, layer.self_attn.k_norm.weight,
-                                            self.rope, slot_positions, layer.self_attn.q_norm.eps)
+                                            self_qn, self_kn, self.rope, slot_positions, layer.self_attn.q_norm.eps)
             y = F.linear(attn.view(tokens, self.dim), layer.self_attn.o_proj.weight)
             hidden, h = ops.adaln_residual(hidden, y, g_self, (c_scale, c_shift), layer.cross_attn_adaln.eps,
                                            x_out=hidden)
             query = F.linear(h, layer.cross_attn.q_proj.weight).view(tokens, heads, hd)
-            prologue = ops.Prologue(layer.cross_attn.q_norm.weight, self.rope, slot_positions,
-                                    layer.cross_attn.q_norm.eps)
+            prologue = ops.Prologue(cross_qn, self.rope, slot_positions, layer.cross_attn.q_norm.eps)
             ctx = ops.block_attention_paged(query, caches[i], cu, seqused_k, block_table, k, self.max_model_len,
                                             self.scale, prologue=prologue, plan=plan)
             y = F.linear(ctx.view(tokens, self.dim), layer.cross_attn.o_proj.weight)

@@ -445,6 +445,12 @@ int fm_noise_rows(const float *z, int64_t rows, int32_t hidden, int64_t z_stride
  * returns the summed milliseconds and the number of launches, then clears them.
  */
 int fm_profile_enable(int enable);
+/* Measurement hook, no reference counterpart: one wavefront on `stream` spins for
+ * spin_ticks (at most 2^24) ticks of the shader-clock counter and stores, at out[0] and
+ * out[1] (device, 16-byte aligned), the shader-clock ticks and the 100 MHz real-time ticks
+ * that passed: their ratio is the shader clock (SCLK) at that point of the stream. Used
+ * to follow the clock under sustained load. */
+int fm_clock_probe(uint64_t *out, uint64_t spin_ticks, void *stream);
 int fm_profile_read(double *total_ms, int64_t *launches);
 
 #ifdef __cplusplus
