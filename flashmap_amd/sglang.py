@@ -197,3 +197,21 @@ def register(namespace: str = NAMESPACE) -> dict[str, object]:
 __all__ = ["block_self_attention", "cross_attention_schedule", "fused_kv_norm_rope_write",
            "kv_norm_rope_write_fp8", "paged_cross_attention", "paged_cross_attention_fp8", "register",
            "rms_norm_rope", "rope_freqs", "sample_rows"]
+
+
+def plugin() -> None:
+    """The SGLang plugin (`sglang.srt.plugins`) entry point of this package (``pyproject.toml``), called
+    by the engine at start-up in every process: defines the ops under the reference's
+    namespace ``flashmap_sglang``, unless ops of that namespace exist already (the reference's
+    own plugin registered first); never raises, as an engine plugin must not."""
+    import logging
+
+    try:
+        getattr(torch.ops, NAMESPACE).rms_norm_rope
+        return  # the namespace is taken
+    except (AttributeError, RuntimeError):
+        pass
+    try:
+        register()
+    except Exception as err:  # noqa: BLE001 -- a plugin must not take the engine down
+        logging.getLogger(__name__).warning("flashmap_amd: flashmap_sglang ops not registered: %s", err)

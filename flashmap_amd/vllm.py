@@ -207,3 +207,21 @@ def register(namespace: str = NAMESPACE) -> dict[str, object]:
 __all__ = ["block_self_attention", "cross_attention_schedule", "paged_cross_attention",
            "paged_cross_attention_runs", "register", "rms_norm_rope", "seeded_normal", "split_argmax",
            "write_context_kv"]
+
+
+def plugin() -> None:
+    """The vLLM general plugin (`vllm.general_plugins`) entry point of this package (``pyproject.toml``), called
+    by the engine at start-up in every process: defines the ops under the reference's
+    namespace ``flashmap_vllm``, unless ops of that namespace exist already (the reference's
+    own plugin registered first); never raises, as an engine plugin must not."""
+    import logging
+
+    try:
+        getattr(torch.ops, NAMESPACE).rms_norm_rope
+        return  # the namespace is taken
+    except (AttributeError, RuntimeError):
+        pass
+    try:
+        register()
+    except Exception as err:  # noqa: BLE001 -- a plugin must not take the engine down
+        logging.getLogger(__name__).warning("flashmap_amd: flashmap_vllm ops not registered: %s", err)
