@@ -14,7 +14,8 @@
 // unit's partials (the LSE merge of flashmap/sglang/verify_attention.py:184-233) and
 // writes the bf16 output.
 //
-// Three launches per call:
+// Three launches per call (two when the units are at most half the shares: the
+// streaming kernel then reads the caller's query rows and applies the prologue itself):
 //   pack_queries_kernel  the query rows of every unit, in the order the MFMA blocks
 //                        consume them, with the optional QK-RMSNorm + RoPE prologue
 //                        applied (invalid rows are zero): the streaming kernel then
@@ -22,6 +23,10 @@
 //                        prefetch them ahead of the unit
 //   attn_fwd_kernel      the K/V stream and the online softmax
 //   attn_combine_kernel  the merge and the scatter into the caller's output layout
+// Small calls (the whole K/V within one pass of 8-tile workgroups over the CUs: batch 1
+// at a few thousand positions) run attn_small_kernel in place of the first two: one
+// workgroup per share of a few tiles, all of its loads issued at once, the caller's rows
+// read directly; the combine is the same.
 //
 // Workgroup = one wavefront per 16-row block of the unit (4 at GQA 4 x 16 rows). All
 // wavefronts walk the share's tiles together: K/V tiles stream from HBM straight into
@@ -36,7 +41,9 @@
 //   online softmax on S^T:    each lane owns one row (lane % 16): the running max, sum
 //                             and rescale are lane-local; the max crosses 4 lane groups
 //   O^T[d][r] += V^T P^T      B = P^T is the S^T accumulator rounded to bf16 as is;
-//                             A = V^T is read transposed out of LDS (16-bit reads)
+//                             A = V^T is read transposed out of LDS with
+//                             ds_read_b64_tr_b16 (ds_read_b64_tr_b8 + an exact
+//                             widening to bf16 for e4m3 V)
 // so no wavefront exchanges data with another and each writes its own rows.
 #include <math.h>
 #include <stddef.h>
@@ -1653,6 +1660,127 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   block_sync();
 }
 
+// Small calls: a few units split over many shares (one sequence at batch 1, a handful at
+// most), whose whole K/V fits one pass of workgroups over the CUs. One workgroup per share
+// of at most SMALL_TILES tiles, W consumer wavefronts (one per 16-row block of the unit),
+// no producer and no ring: the share's page ids, then all of its K/V loads are issued at
+// once into stages of their own (the persistent kernel's stage layout), the first
+// segment's query rows are loaded (the caller's rows with the prologue applied by the
+// query pass's code, or the packed rows) while the tiles fly, and the tiles are computed
+// in order. The same line of tiles, shares and partial slots as attn_fwd_kernel, so the
+// combine merges the partials unchanged. A share of several units loads each further
+// unit's query rows at its segment start.
+constexpr int SMALL_TILES = 8;  // stages per workgroup: 8 x 17.2 KB of LDS at head_dim 128
+
+template <int D>
+__device__ __forceinline__ void small_query_rows(const AttnArgs &a, int64_t unit, int r, int g,
+                                                 u32x4_t (&qf)[D / 32], bool direct) {
+  constexpr int KT = D / 32;
+  typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
+  if (!direct) {  // packed by the query pass (prologue applied, invalid rows zero)
+    const uint16_t *src = a.qp + (unit * 16 * a.nrb + r) * D + 8 * g;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) qf[t] = *(g_u32x4_t *)(src + 32 * t);
+    return;
+  }
+  const int b = (int)(unit / a.ups);
+  const int ul = (int)(unit - (int64_t)b * a.ups);
+  const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
+  const int R = rg * 16 * a.nrb + r;
+  const int gq = R / a.q_len, tq = R - gq * a.q_len;
+  const bool valid = gq < a.group && tq < q_rows_of(a, b);
+  const int64_t tok = q_token_index(a, b, valid ? tq : 0);
+  const int64_t head = (int64_t)h * a.group + (valid ? gq : 0);
+  const uint16_t *src = a.q + (a.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)(valid ? tq : 0) * a.q_st) +
+                        head * a.q_sh + 8 * g;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) qf[t] = valid ? *(g_u32x4_t *)(src + 32 * t) : u32x4_t{0, 0, 0, 0};
+  if (a.qn_w != nullptr) {
+    const int64_t rr = clamp_row(a.rope, valid ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
+    norm_rope_row<D>(qf, a.qn_w, a.eps, a.rope, rr, g);  // every lane: the norm crosses lanes
+  }
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
+    if (!valid) qf[t] = u32x4_t{0, 0, 0, 0};
+}
+
+template <int LAYOUT, int W, int D, bool DIRECT>
+__global__ __launch_bounds__(64 * W) void attn_small_kernel(const AttnArgs a, const int32_t *__restrict__ table,
+                                                            const int32_t *__restrict__ plan,
+                                                            const int32_t *__restrict__ seqlens) {
+  using G = Geo<D>;
+  constexpr int KPW = (G::NI + W - 1) / W;  // this wavefront's loads per tile
+  constexpr bool IDS = LAYOUT != CONTIG;
+  __shared__ __attribute__((aligned(1024))) char stages[SMALL_TILES * G::STAGE];
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 15, g = lane >> 4;
+  SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens, nullptr, false};
+  const int64_t total = (int64_t)a.ups * sm.prefix(a, a.batch);
+  const int share = (int)blockIdx.x;
+  const int64_t T0 = share_start(share, total, a.num_shares);
+  const int ntiles = (int)(share_start(share + 1, total, a.num_shares) - T0);
+  if (ntiles <= 0) return;  // uniform over the workgroup
+  auto stage = [&](int t) { return stages + (t % SMALL_TILES) * G::STAGE; };
+  Cursor cc = cursor_at(a, sm, T0);
+  Cursor ct = cc;  // paged layouts: the next tile whose page ids are loaded
+  Loader ld;       // the next tile whose K/V are loaded
+  ld.c = cc;
+  loader_unit<LAYOUT>(a, ld);
+  uint32_t loff[KPW];
+#pragma unroll
+  for (int k = 0; k < KPW; ++k) {
+    int row, coff, dst;
+    bool isk;
+    const int i = wave + k * W;
+    load_slot<D>(i < G::NI ? i : 0, lane, row, coff, isk, dst);
+    loff[k] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + (uint32_t)coff;
+  }
+  const int r = wave * 16 + n;
+  u32x4_t qf[G::KT];
+  f32x4_t acc[G::DB];
+  float m = -INFINITY, l = 0.f;
+  // The host sizes shares to at most SMALL_TILES tiles (one chunk); a longer share (lengths
+  // past max_seqlen_k) is walked in chunks of SMALL_TILES stages.
+  for (int c0 = 0; c0 < ntiles; c0 += SMALL_TILES) {
+    const int c1 = ntiles - c0 < SMALL_TILES ? ntiles : c0 + SMALL_TILES;
+    if (c0 > 0) block_sync();  // every wavefront is done with the stages being reloaded
+    if (IDS) {  // the chunk's page ids: tile j's by wavefront j % W, awaited and published
+      for (int j = c0; j < c1; ++j) {
+        if (j % W == wave) issue_ids<LAYOUT, D>(a, table, ct, stage(j), lane);
+        if (j + 1 < ntiles) cursor_next(a, sm, ct);
+      }
+      wait_vm<0>();
+      block_sync();
+    }
+    for (int j = c0; j < c1; ++j) {  // every K/V load of the chunk: load i of a tile by wavefront i % W
+      issue_kv<LAYOUT, D, W>(a, ld, stage(j), wave, lane, loff);
+      if (j + 1 < ntiles) loader_advance<LAYOUT>(a, sm, ld);
+    }
+    if (c0 == 0) small_query_rows<D>(a, cc.u, r, g, qf, DIRECT);  // while the tiles fly
+    wait_vm<0>();
+    block_sync();
+    for (int i = c0; i < c1; ++i) {
+      if (i == 0 || cc.lt == 0) {  // a segment starts: a fresh accumulator (rows of a further unit)
+        if (i > 0) small_query_rows<D>(a, cc.u, r, g, qf, DIRECT);
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        m = -INFINITY;
+        l = 0.f;
+      }
+      compute_tile<D, false>(a, stage(i), qf, a.scale_log2, acc, m, l, cc.lt * G::T, cc.L, lane);
+      if (cc.lt == cc.tiles - 1 || i == ntiles - 1) {  // the segment ends: its partial
+        const float lt_sum = sum_over_groups(l);
+        const float inv = lt_sum > 0.f ? 1.f / lt_sum : 0.f;
+        const float lse = m + log2f(lt_sum);
+        u32x2_t h[G::DB];
+        const float sc = make_partial<D>(acc, inv, h);
+        store_partial_rows<D>(a, h, lse, sc, ((int64_t)cc.u + share) * (16 * W) + r, g);
+      }
+      if (i + 1 < ntiles) cursor_next(a, sm, cc);
+    }
+  }
+}
+
 // Running log2-domain LSE merge of one thread's 8 channels of an output row: acc and den
 // are the segments' values and softmax masses, both relative to exp2(M).
 struct RowMerge {
@@ -1698,13 +1826,19 @@ __device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, 
   const int64_t wa = share_of(U0, total, nw);
   const int nseg = (int)(share_of(U0 + tiles_b - 1, total, nw) - wa) + 1;
   const int64_t row0 = (unit + wa) * rows + r;
+  // More shares than tiles (lengths far below max_seqlen_k, or the small-call kernel's
+  // shares of a few tiles): some shares are empty and write nothing, so their slots hold
+  // another call's (or another unit's) data and are skipped. With total >= nw every share
+  // holds a tile.
+  const bool sparse = nw > total;
   for (int s0 = 0; s0 < nseg; s0 += MB) {
     f32x2_t ls[MB];
     u32x4_t ow[MB];
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int64_t row = row0 + (int64_t)(s0 + j) * rows;
-      const bool in = s0 + j < nseg;
+      const int64_t w = wa + s0 + j;
+      const bool in = s0 + j < nseg && (!sparse || share_start(w + 1, total, nw) > share_start(w, total, nw));
       ls[j] = in ? *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row) : f32x2_t{-INFINITY, 1.f};
       ow[j] = in ? load16(a.part_o + row * D + 8 * c) : u32x4_t{0, 0, 0, 0};
     }
@@ -1850,6 +1984,30 @@ static int dq_seq_cap(int w) {
   }
 }
 
+template <int LAYOUT, int D>
+static AttnKernel pick_small(int w) {
+  switch (w) {
+    case 2: return attn_small_kernel<LAYOUT, 2, D, true>;
+    case 4: return attn_small_kernel<LAYOUT, 4, D, true>;
+    case 5: return attn_small_kernel<LAYOUT, 5, D, true>;
+    case 8: return attn_small_kernel<LAYOUT, 8, D, true>;
+    default: return nullptr;
+  }
+}
+
+// The small-call kernel for (layout, head_dim, row blocks per unit), or NULL where it has
+// no instance (row blocks other than 2, 4, 5, 8).
+static AttnKernel select_small(int layout, int d, int w) {
+  if (d == 128) {
+    if (layout == CONTIG) return pick_small<CONTIG, 128>(w);
+    if (layout == PAGED16) return pick_small<PAGED16, 128>(w);
+    return pick_small<PAGED, 128>(w);
+  }
+  if (layout == CONTIG) return pick_small<CONTIG, 64>(w);
+  if (layout == PAGED16) return pick_small<PAGED16, 64>(w);
+  return pick_small<PAGED, 64>(w);
+}
+
 static AttnKernel select_kernel(int layout, int d, int w, int qmode) {
   if (qmode == Q_F8) {
     if (d == 128) return layout == PAGED16 ? pick_kernel<PAGED16, 128, true, false>(w) : pick_kernel<PAGED, 128, true, false>(w);
@@ -1919,7 +2077,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // tail: a verify call (one more partial slot per unit, for its verify tokens). qmode: how
 // the queries reach the consumers (Q_DIRECT needs no packed rows in the workspace).
 static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int max_k,
-                  bool need_plan, Sizing *sz, bool tail = false, int qmode = Q_PACKED) {
+                  bool need_plan, Sizing *sz, bool tail = false, int qmode = Q_PACKED, int small_tiles = 0) {
   DeviceInfo info;
   int rc = device_info(&info);
   if (rc != FM_OK) return rc;
@@ -1938,6 +2096,10 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   if (nw < 1) nw = 1;
   sz->num_wg = (int)nw;
   sz->num_shares = (int)nw * r;
+  if (small_tiles > 0) {  // the small-call kernel: one workgroup per share of <= small_tiles tiles
+    const int64_t shares = (tiles_bound + small_tiles - 1) / small_tiles;
+    sz->num_wg = sz->num_shares = (int)(shares > 0 ? shares : 1);
+  }
   const size_t rows = (size_t)sz->rp.nrb * 16;
   const size_t units = (size_t)batch * ups;
   const size_t slots = units + (size_t)sz->num_shares + (tail ? units : 0);  // unit + share; tails
@@ -1954,6 +2116,23 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   off = align256(off + sizeof(uint16_t) * slots * rows * d);
   sz->bytes = off;
   return FM_OK;
+}
+
+// Tiles per share of attn_small_kernel for a bf16 call without verify tokens, or 0 where
+// the persistent kernel runs: the small kernel takes calls whose K/V fits one pass of
+// SMALL_TILES-tile workgroups over the CUs and whose row blocks per unit it has an
+// instance for. FLASHMAP_SMALL_TILES sets the tiles per share (1 .. SMALL_TILES, default
+// 4); 0 turns the kernel off.
+static int small_tiles_for(int layout, int batch, int q_len, int hq, int hkv, int d, int max_k) {
+  DeviceInfo info;
+  if (device_info(&info) != FM_OK) return 0;
+  const RowPlan rp = row_plan(hq / hkv, q_len);
+  const int64_t tiles_bound = (int64_t)hkv * rp.rgroups * batch * (((int64_t)max_k + TILE - 1) / TILE);
+  int tps = env_int("FLASHMAP_SMALL_TILES", 4);
+  tps = tps > SMALL_TILES ? SMALL_TILES : tps;
+  if (tps <= 0 || tiles_bound > (int64_t)info.cus * SMALL_TILES || select_small(layout, d, rp.nrb) == nullptr)
+    return 0;
+  return tps;
 }
 
 static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -2040,7 +2219,22 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     const bool small = units * 2 <= sz.num_shares;
     if (fast_rope && c.batch <= cap && (force == 0 || (force < 0 && small))) qmode = Q_DIRECT;
   }
-  if (qmode == Q_DIRECT) {
+  // Small calls: attn_small_kernel with the caller's rows read directly (two launches),
+  // unless the workspace was sized for the persistent kernel only (a static scratch).
+  int small_tiles = (!a.f8 && vf == nullptr) ? small_tiles_for(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k)
+                                             : 0;
+  if (small_tiles > 0) {
+    Sizing ss;
+    rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &ss, false, Q_DIRECT, small_tiles);
+    if (rc != FM_OK) return rc;
+    if (ss.bytes <= c.ws_bytes) {
+      sz = ss;
+      qmode = Q_DIRECT;
+    } else {
+      small_tiles = 0;
+    }
+  }
+  if (small_tiles == 0 && qmode == Q_DIRECT) {
     rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, qmode);
     if (rc != FM_OK) return rc;
   }
@@ -2111,12 +2305,13 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     pack_queries_kernel<64, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
   }
   if (qmode != Q_DIRECT) FM_CHECK_HIP(hipGetLastError());
-  AttnKernel k = select_kernel(layout, c.d, sz.rp.nrb, qmode);
+  AttnKernel k = small_tiles > 0 ? select_small(layout, c.d, sz.rp.nrb) : select_kernel(layout, c.d, sz.rp.nrb, qmode);
+  const dim3 kblock(small_tiles > 0 ? 64 * sz.rp.nrb : 64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb));
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
-  const hipError_t lerr = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(sz.num_wg),
-                                          dim3(64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb)), kargs, 0, c.stream);
+  const hipError_t lerr = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(sz.num_wg), kblock, kargs, 0,
+                                          c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
   // One workgroup of 2 D threads per 16-row block; units split into many segments (a
@@ -2163,7 +2358,9 @@ extern "C" size_t fm_attn_workspace_bytes(int32_t batch, int32_t max_seqlen_q, i
   if (hipGetDevice(&prev) != hipSuccess) return 0;
   if (device != prev && hipSetDevice(device) != hipSuccess) return 0;
   // The largest need over the three layouts (their occupancy, hence grid, may differ),
-  // with room for an in-call plan.
+  // with room for an in-call plan; calls the small-call kernel takes at the largest share
+  // count any FLASHMAP_SMALL_TILES gives (one tile per share: at most CUs x SMALL_TILES
+  // shares).
   size_t bytes = 0;
   int rc = FM_OK;
   for (int v = 0; v < 5 && rc == FM_OK; ++v) {  // the three layouts, then the two fp8 ones
@@ -2172,6 +2369,14 @@ extern "C" size_t fm_attn_workspace_bytes(int32_t batch, int32_t max_seqlen_q, i
     rc = sizing(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, max_seqlen_k,
                 true, &sz, false, v >= 3 ? Q_F8 : Q_PACKED);
     if (rc == FM_OK && sz.bytes > bytes) bytes = sz.bytes;
+    const int st = v < 3 ? small_tiles_for(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim,
+                                           max_seqlen_k)
+                         : 0;
+    if (rc == FM_OK && st > 0) {  // the small-call kernel at one tile per share: the most shares
+      rc = sizing(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, max_seqlen_k, true, &sz,
+                  false, Q_DIRECT, 1);
+      if (rc == FM_OK && sz.bytes > bytes) bytes = sz.bytes;
+    }
   }
   if (device != prev) hipSetDevice(prev);
   return rc == FM_OK ? bytes : 0;

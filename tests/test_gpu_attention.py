@@ -362,6 +362,7 @@ def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
             return o.block_attention_contig(q_pre.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev),
                                             seqlens_k=lens.to(dev), prologue=pro)
     outs = {}
+    monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")  # the persistent kernel (the small-call one reads rows directly)
     for mode in ("1", "0"):
         monkeypatch.setenv("FLASHMAP_QUERY_PASS", mode)
         outs[mode] = run()
@@ -374,3 +375,53 @@ def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
             s, e = i * t, (i + 1) * t
         want = ref.attention(qn[s:e].transpose(0, 1), k[i, :, : int(lens[i])], v[i, :, : int(lens[i])])
         check_close(got[s:e], want.transpose(0, 1))
+
+
+@pytest.mark.parametrize("layout", ["contig", "paged"])
+@pytest.mark.parametrize("hq,hkv,lens", [(8, 2, [700, 33, 0, 260]), (32, 8, [1100, 5])])
+def test_small_call_kernel(dev, monkeypatch, layout, hq, hkv, lens):
+    """Calls whose K/V fits one pass of a few-tile workgroups over the CUs run the small-call
+    kernel: against the oracle at 1, 3 and 8 tiles per share and with that kernel off (the
+    persistent one), max_seqlen_k far above the lengths (more shares than tiles, so empty
+    shares whose partial slots the merge must skip), ragged draft rows, an empty context
+    and the fused prologue."""
+    g = gen(43)
+    d, t, page, max_k = 128, 16, 16, 4096
+    lens = torch.tensor(lens)
+    b = len(lens)
+    k = normed_keys(b, hkv, max_k, d, g)
+    v = torch.randn(b, hkv, max_k, d, generator=g).bfloat16()
+    q_pre = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table, make = _tables("interleaved", int(lens.max()) + t + 1, d)
+    rope = make(table.to(dev))
+    rows = torch.tensor([16, 9, 16, 3][:b]) if layout == "paged" else torch.full((b,), t)
+    cu = torch.cat([torch.zeros(1, dtype=torch.int32), rows.cumsum(0).to(torch.int32)])
+    pos = torch.cat([int(n) + torch.arange(int(r)) for n, r in zip(lens, rows)])
+    n_tok = int(cu[-1])
+    o = ops()
+    pro = o.Prologue(w.to(dev), rope, pos.to(dev), 1e-6)
+    if layout == "paged":
+        bt, total = paged_layout(lens, page, g)
+        cache = vllm_cache_from_contig(k, v, lens, page, bt, total).to(dev)
+
+        def run():
+            return o.block_attention_paged(q_pre[:n_tok].to(dev), cache, cu.to(dev), lens.to(dev, torch.int32),
+                                           bt.to(dev), t, max_k, d ** -0.5, prologue=pro)
+    else:
+        def run():
+            return o.block_attention_contig(q_pre.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev),
+                                            seqlens_k=lens.to(dev), prologue=pro)
+    qn = ref.rms_norm_rope_vllm(q_pre[:n_tok], w, table, pos, 1e-6)
+    for tiles in ("1", "3", "8", "0"):
+        monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
+        got = run().cpu().view(-1, hq, d)
+        print(f"small-call kernel {layout} hq={hq} hkv={hkv} lens={lens.tolist()} tiles per share={tiles}",
+              flush=True)
+        for i in range(b):
+            s, e = (int(cu[i]), int(cu[i + 1])) if layout == "paged" else (i * t, (i + 1) * t)
+            if int(lens[i]) == 0:
+                assert (got[s:e] == 0).all(), "an empty context gives zeros"
+                continue
+            want = ref.attention(qn[s:e].transpose(0, 1), k[i, :, : int(lens[i])], v[i, :, : int(lens[i])])
+            check_close(got[s:e], want.transpose(0, 1))
