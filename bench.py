@@ -467,11 +467,13 @@ CONTIG_WORKLOADS = {
 
 
 def run_contig(args, dev) -> dict:
-    """One call = the split-KV attention with the query prologue applied in the kernel,
-    and the combine, on contiguous (batch, kv heads, positions, head_dim) keys and values
-    (FlashMapCache views). Latency-bound at batch 1: timed as a graph replay after an
-    L2 / Infinity Cache flush (see _flushed)."""
+    """One call = the block attention with the query prologue applied in the kernel, on
+    contiguous (batch, kv heads, positions, head_dim) keys and values (FlashMapCache
+    views), the rotary angles as FlashMapAttention.forward passes them: one (cos, sin)
+    row per draft token. Latency-bound at batch 1: timed call by call after an L2 /
+    Infinity Cache flush (see _flushed)."""
     from flashmap_amd import ops
+    from flashmap_amd.drafter import _token_rope, rope_tables
     from oracle import attention as ref
 
     batch, hq, hkv, d, k_rows, ctx = CONTIG_WORKLOADS[args.workload]
@@ -483,7 +485,8 @@ def run_contig(args, dev) -> dict:
     qpos = (ctx + torch.arange(k_rows)).repeat(batch)
     w = torch.ones(d)
     qd, kd, vd = q.to(dev), keys.to(dev), values.to(dev)
-    pro = ops.Prologue(w.to(dev), ops.rope_from_table(table.to(dev)), qpos.to(dev), 1e-6)
+    rope = _token_rope(rope_tables(qpos.view(batch, k_rows).to(dev), d, 1e6), batch, k_rows)
+    pro = ops.Prologue(w.to(dev), rope, None, 1e-6)
     out = torch.empty_like(qd)
 
     def call():
@@ -501,8 +504,9 @@ def run_contig(args, dev) -> dict:
         "dtype": "bf16", "data": "synthetic: seeded CPU draw (q, K, V)",
         "config": {"workload": args.workload, "batch": batch, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
                    "block_queries": k_rows, "ctx": ctx, "layout": "contiguous (batch, kv_heads, ctx, head_dim)",
-                   "prologue": "QK-RMSNorm + RoPE inside the attention kernel (no query pass)"},
-        "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                   "prologue": "QK-RMSNorm + RoPE inside the attention kernel (no query pass), "
+                               "one (cos, sin) row per draft token as FlashMapAttention passes them"},
+        "roofline": {"bound": "hbm", "kernel": "attn_small_kernel", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": total,
                      "kernel_us": round(kernel_ms * 1e3, 2)},
         "warm_us_per_call": round(t["warm_ms"] * 1e3, 2),

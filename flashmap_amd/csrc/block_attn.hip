@@ -557,12 +557,121 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
   }
 }
 
+// O^T += V^T P^T for one tile, in two steps so that the V reads fly while the softmax
+// runs: pv_issue starts the reads of the tile's V^T operands (vbase: the tile's V blocks
+// in the stage layout), pv_finish awaits them and accumulates with pk, this lane's bf16
+// P^T values (row n, positions 16 pb + 4 g + i). Between the two, the caller issues no
+// LDS or scalar memory operation of its own.
 template <int D>
-__device__ __forceinline__ void pv_accumulate(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
-                                              int lane);
+struct VFrags {
+  u32x2_t w[2][D / 16];
+};
+
 template <int D>
-__device__ __forceinline__ void pv_accumulate_f8(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
-                                                 int lane);
+__device__ __forceinline__ void pv_issue(const char *vbase, VFrags<D> &v, int lane) {
+  using G = Geo<D>;
+  const int n = lane & 15, g = lane >> 4;
+  // V^T operand: row d = 16 db + n, reduction positions pos(g, j) = 4g + j (j < 4) and
+  // 16 + 4g + j - 4 (j >= 4), the positions of this lane's S^T values. Two
+  // ds_read_b64_tr_b16 per operand: within each 16-lane group, lane l receives slot j
+  // from element l % 4 of the 8 bytes lane 4j + l / 4 addressed; so lane s addresses
+  // row 16h + 4g + s/4 at channels 16db + 4(s%4) .. +3.
+  const int s4 = n >> 2, c4 = n & 3;
+  int vb[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int r = 16 * hh + 4 * g + s4;
+    const int blk = (r & 3) + 4 * (r / (4 * G::RPB)), slot = (r % (4 * G::RPB)) >> 2;
+    vb[hh] = blk * G::VPITCH + slot * (2 * D) + 8 * c4;
+  }
+  // The reads are issued as inline asm with their own lgkmcnt wait: through the
+  // builtin, the compiler cannot tell them apart from the LDS-DMA writes still in
+  // flight for later tiles and drains those (vmcnt(0)) before every tile's P.V.
+  typedef __attribute__((address_space(3))) const char lds_char_t;
+  const uint32_t a0 = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + vb[0]);
+  const uint32_t a1 = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + vb[1]);
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db) {
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v.w[0][db]) : "v"(a0), "i"(32 * db));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v.w[1][db]) : "v"(a1), "i"(32 * db));
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void pv_finish(VFrags<D> &v, const u32x4_t &pk, f32x4_t (&acc)[D / 16]) {
+  using G = Geo<D>;
+  static_assert(G::DB == 8 || G::DB == 4, "head_dim 128 or 64");
+  if constexpr (G::DB == 8) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v.w[0][0]), "+v"(v.w[1][0]), "+v"(v.w[0][1]), "+v"(v.w[1][1]), "+v"(v.w[0][2]),
+                   "+v"(v.w[1][2]), "+v"(v.w[0][3]), "+v"(v.w[1][3]), "+v"(v.w[0][4]), "+v"(v.w[1][4]),
+                   "+v"(v.w[0][5]), "+v"(v.w[1][5]), "+v"(v.w[0][6]), "+v"(v.w[1][6]), "+v"(v.w[0][7]),
+                   "+v"(v.w[1][7]));
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v.w[0][0]), "+v"(v.w[1][0]), "+v"(v.w[0][1]), "+v"(v.w[1][1]), "+v"(v.w[0][2]),
+                   "+v"(v.w[1][2]), "+v"(v.w[0][3]), "+v"(v.w[1][3]));
+  }
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db) {
+    const u32x4_t vf = {v.w[0][db][0], v.w[0][db][1], v.w[1][db][0], v.w[1][db][1]};
+    acc[db] = mfma_16x16x32(vf, pk, acc[db]);
+  }
+}
+
+
+// e4m3 V in the F8 stage layout: one ds_read_b64_tr_b8 per 16-channel block gives lane
+// (n, g) V[pos(g, j)][16 db + n] for j < 8 (pos(g, j) = 4 g + j, then 16 + 4 g + j - 4:
+// the positions of its P^T values). Within a 16-lane group the read hands lane s, in
+// slot j, byte s % 8 of the 8 bytes lane 2 j + s / 8 addressed, so lane s addresses row
+// pos(g, s / 2) at channels 16 db + 8 (s % 2). The e4m3 values are exact in bf16.
+// pv_issue_f8 starts one 32-position half's reads (vbase: the half's rows), pv_finish_f8
+// awaits both halves' reads (at its first half) and accumulates half h with pk.
+template <int D>
+struct VFragsF8 {
+  u32x2_t w[2][D / 16];
+};
+
+template <int D>
+__device__ __forceinline__ void pv_issue_f8(const char *vbase, u32x2_t (&w)[D / 16], int lane) {
+  using G = Geo<D, true>;
+  const int n = lane & 15, g = lane >> 4;
+  const int j = n >> 1;
+  const int r = j < 4 ? 4 * g + j : 12 + 4 * g + j;  // pos(g, j)
+  const uint32_t sw16 = 16u * (uint32_t)((r / G::R256) % G::LPR);
+  typedef __attribute__((address_space(3))) const char lds_char_t;
+  const uint32_t base = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + (r / G::RPB) * G::VPITCH + (r % G::RPB) * G::RB +
+                                                             8 * (n & 1));
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db)
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(w[db]) : "v"(base + (sw16 ^ (16u * db))));
+}
+
+template <int D>
+__device__ __forceinline__ void pv_finish_f8(VFragsF8<D> &v, int h, const u32x4_t &pk, f32x4_t (&acc)[D / 16]) {
+  using G = Geo<D, true>;
+  static_assert(G::DB == 8 || G::DB == 4, "head_dim 128 or 64");
+  if (h == 0) {  // both halves' reads
+    if constexpr (G::DB == 8) {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(v.w[0][0]), "+v"(v.w[0][1]), "+v"(v.w[0][2]), "+v"(v.w[0][3]), "+v"(v.w[0][4]),
+                     "+v"(v.w[0][5]), "+v"(v.w[0][6]), "+v"(v.w[0][7]), "+v"(v.w[1][0]), "+v"(v.w[1][1]),
+                     "+v"(v.w[1][2]), "+v"(v.w[1][3]), "+v"(v.w[1][4]), "+v"(v.w[1][5]), "+v"(v.w[1][6]),
+                     "+v"(v.w[1][7]));
+    } else {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(v.w[0][0]), "+v"(v.w[0][1]), "+v"(v.w[0][2]), "+v"(v.w[0][3]), "+v"(v.w[1][0]),
+                     "+v"(v.w[1][1]), "+v"(v.w[1][2]), "+v"(v.w[1][3]));
+    }
+  }
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db) {
+    const u32x2_t w = v.w[h][db];
+    const u32x4_t vf = {e4m3x2_to_bf16x2(w[0], false), e4m3x2_to_bf16x2(w[0], true),
+                        e4m3x2_to_bf16x2(w[1], false), e4m3x2_to_bf16x2(w[1], true)};
+    acc[db] = mfma_16x16x32(vf, pk, acc[db]);
+  }
+}
 
 // One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T. sl:
 // this lane's row's score scale in log2 units (softmax_scale log2(e), times the row's
@@ -577,29 +686,72 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
   constexpr int NH = G::NH;  // 16-position blocks of the tile
   const int g = lane >> 4;
   f32x4_t s[NH];
+  VFrags<D> vq;  // bf16: the tile's V^T operands, read while the softmax runs
+  if constexpr (!F8) {
+    // Every K fragment of the tile in flight at once, then the MFMAs (left to itself, the
+    // compiler waits for each read before its MFMA: eight LDS round trips per tile).
+    constexpr int NK = NH * G::KC;
+    static_assert(NK == 8 || NK == 4, "head_dim 128 or 64");
+    typedef __attribute__((address_space(3))) const char lds_char_t;
+    const uint32_t ka = (uint32_t)(uintptr_t)(lds_char_t *)(stage + lane * 16);
+    u32x4_t kf[NK];
 #pragma unroll
-  for (int pb = 0; pb < NH; ++pb) {
-    f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (F8 && G::KC == 2) {  // head_dim 128: one 128-channel fp8 MFMA
-      const u32x4_t k0 = *reinterpret_cast<const u32x4_t *>(stage + (pb * 2) * 1024 + lane * 16);
-      const u32x4_t k1 = *reinterpret_cast<const u32x4_t *>(stage + (pb * 2 + 1) * 1024 + lane * 16);
-      const i32x8_t ka = {(int)k0[0], (int)k0[1], (int)k0[2], (int)k0[3], (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
-      const i32x8_t qb = {(int)qf[0][0], (int)qf[0][1], (int)qf[0][2], (int)qf[0][3],
-                          (int)qf[1][0], (int)qf[1][1], (int)qf[1][2], (int)qf[1][3]};
-      c = mfma_16x16x128_f8(ka, qb, c);
+    for (int i = 0; i < NK; ++i) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[i]) : "v"(ka), "i"(1024 * i));
+    if constexpr (NK == 8) {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]),
+                     "+v"(kf[7]));
     } else {
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]));
+    }
 #pragma unroll
-      for (int t = 0; t < G::KC; ++t) {
-        const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(stage + (pb * G::KC + t) * 1024 + lane * 16);
-        if constexpr (F8) {
-          c = mfma_16x16x32_f8(u32x2_t{kf[0], kf[1]}, u32x2_t{qf[t][0], qf[t][1]}, c);
-          c = mfma_16x16x32_f8(u32x2_t{kf[2], kf[3]}, u32x2_t{qf[t][2], qf[t][3]}, c);
-        } else {
-          c = mfma_16x16x32(kf, qf[t], c);
+    for (int pb = 0; pb < NH; ++pb) {
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < G::KC; ++t) c = mfma_16x16x32(kf[pb * G::KC + t], qf[t], c);
+      s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
+    }
+    pv_issue<D>(stage + G::KBYTES, vq, lane);
+  }
+  VFragsF8<D> vq8;  // e4m3: the tile's V^T operands (both 32-position halves)
+  if constexpr (F8) {
+    // As for bf16: every K fragment in flight at once, then the MFMAs.
+    constexpr int NK = NH * G::KC;
+    static_assert(NK == 8 || NK == 4, "head_dim 128 or 64");
+    typedef __attribute__((address_space(3))) const char lds_char_t;
+    const uint32_t ka = (uint32_t)(uintptr_t)(lds_char_t *)(stage + lane * 16);
+    u32x4_t kf[NK];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[i]) : "v"(ka), "i"(1024 * i));
+    if constexpr (NK == 8) {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]),
+                     "+v"(kf[7]));
+    } else {
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]));
+    }
+#pragma unroll
+    for (int pb = 0; pb < NH; ++pb) {
+      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (G::KC == 2) {  // head_dim 128: one 128-channel fp8 MFMA
+        const u32x4_t k0 = kf[2 * pb], k1 = kf[2 * pb + 1];
+        const i32x8_t ka8 = {(int)k0[0], (int)k0[1], (int)k0[2], (int)k0[3],
+                             (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
+        const i32x8_t qb = {(int)qf[0][0], (int)qf[0][1], (int)qf[0][2], (int)qf[0][3],
+                            (int)qf[1][0], (int)qf[1][1], (int)qf[1][2], (int)qf[1][3]};
+        c = mfma_16x16x128_f8(ka8, qb, c);
+      } else {
+#pragma unroll
+        for (int t = 0; t < G::KC; ++t) {
+          const u32x4_t k = kf[pb * G::KC + t];
+          c = mfma_16x16x32_f8(u32x2_t{k[0], k[1]}, u32x2_t{qf[t][0], qf[t][1]}, c);
+          c = mfma_16x16x32_f8(u32x2_t{k[2], k[3]}, u32x2_t{qf[t][2], qf[t][3]}, c);
         }
       }
+      s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
     }
-    s[pb] = c;  // S^T[pos 16 pb + 4 g + i][row n]
+#pragma unroll
+    for (int h = 0; h < NH / 2; ++h) pv_issue_f8<D>(stage + G::KBYTES + h * 32 * G::RB, vq8.w[h], lane);
   }
   if (pos0 + G::T > L) {
 #pragma unroll
@@ -640,97 +792,18 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
     const u32x4_t pk = {pack_bf16x2(p[2 * h][0], p[2 * h][1]), pack_bf16x2(p[2 * h][2], p[2 * h][3]),
                         pack_bf16x2(p[2 * h + 1][0], p[2 * h + 1][1]), pack_bf16x2(p[2 * h + 1][2], p[2 * h + 1][3])};
     if constexpr (F8)
-      pv_accumulate_f8<D>(stage + G::KBYTES + h * 32 * G::RB, pk, acc, lane);
+      pv_finish_f8<D>(vq8, h, pk, acc);
     else
-      pv_accumulate<D>(stage + G::KBYTES, pk, acc, lane);
+      pv_finish<D>(vq, pk, acc);
   }
 }
 
-// pv_accumulate for e4m3 V in the F8 stage layout: one ds_read_b64_tr_b8 per 16-channel
-// block gives lane (n, g) V[pos(g, j)][16 db + n] for j < 8 (pos(g, j) = 4 g + j, then
-// 16 + 4 g + j - 4: the positions of its P^T values). Within a 16-lane group the read
-// hands lane s, in slot j, byte s % 8 of the 8 bytes lane 2 j + s / 8 addressed, so lane
-// s addresses row pos(g, s / 2) at channels 16 db + 8 (s % 2). The e4m3 values are exact
-// in bf16.
-template <int D>
-__device__ __forceinline__ void pv_accumulate_f8(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
-                                                 int lane) {
-  using G = Geo<D, true>;
-  const int n = lane & 15, g = lane >> 4;
-  const int j = n >> 1;
-  const int r = j < 4 ? 4 * g + j : 12 + 4 * g + j;  // pos(g, j)
-  const uint32_t sw16 = 16u * (uint32_t)((r / G::R256) % G::LPR);
-  typedef __attribute__((address_space(3))) const char lds_char_t;
-  const uint32_t base = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + (r / G::RPB) * G::VPITCH + (r % G::RPB) * G::RB +
-                                                             8 * (n & 1));
-  u32x2_t w[G::DB];
-#pragma unroll
-  for (int db = 0; db < G::DB; ++db)
-    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(w[db]) : "v"(base + (sw16 ^ (16u * db))));
-  static_assert(G::DB == 8 || G::DB == 4, "head_dim 128 or 64");
-  if constexpr (G::DB == 8) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]));
-  } else {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]));
-  }
-#pragma unroll
-  for (int db = 0; db < G::DB; ++db) {
-    const u32x4_t vf = {e4m3x2_to_bf16x2(w[db][0], false), e4m3x2_to_bf16x2(w[db][0], true),
-                        e4m3x2_to_bf16x2(w[db][1], false), e4m3x2_to_bf16x2(w[db][1], true)};
-    acc[db] = mfma_16x16x32(vf, pk, acc[db]);
-  }
-}
-
-// O^T += V^T P^T for one tile: pk holds this lane's bf16 P^T values (row n, positions
-// 16 pb + 4 g + i), vbase the tile's V blocks in the stage layout.
 template <int D>
 __device__ __forceinline__ void pv_accumulate(const char *vbase, const u32x4_t &pk, f32x4_t (&acc)[D / 16],
                                               int lane) {
-  using G = Geo<D>;
-  const int n = lane & 15, g = lane >> 4;
-  // V^T operand: row d = 16 db + n, reduction positions pos(g, j) = 4g + j (j < 4) and
-  // 16 + 4g + j - 4 (j >= 4), the positions of this lane's S^T values. Two
-  // ds_read_b64_tr_b16 per operand: within each 16-lane group, lane l receives slot j
-  // from element l % 4 of the 8 bytes lane 4j + l / 4 addressed; so lane s addresses
-  // row 16h + 4g + s/4 at channels 16db + 4(s%4) .. +3.
-  const int s4 = n >> 2, c4 = n & 3;
-  int vb[2];
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int r = 16 * hh + 4 * g + s4;
-    const int blk = (r & 3) + 4 * (r / (4 * G::RPB)), slot = (r % (4 * G::RPB)) >> 2;
-    vb[hh] = blk * G::VPITCH + slot * (2 * D) + 8 * c4;
-  }
-  // The reads are issued as inline asm with their own lgkmcnt wait: through the
-  // builtin, the compiler cannot tell them apart from the LDS-DMA writes still in
-  // flight for later tiles and drains those (vmcnt(0)) before every tile's P.V.
-  typedef __attribute__((address_space(3))) const char lds_char_t;
-  const uint32_t a0 = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + vb[0]);
-  const uint32_t a1 = (uint32_t)(uintptr_t)(lds_char_t *)(vbase + vb[1]);
-  u32x2_t w[2][G::DB];
-#pragma unroll
-  for (int db = 0; db < G::DB; ++db) {
-    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(w[0][db]) : "v"(a0), "i"(32 * db));
-    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(w[1][db]) : "v"(a1), "i"(32 * db));
-  }
-  static_assert(G::DB == 8 || G::DB == 4, "head_dim 128 or 64");
-  if constexpr (G::DB == 8) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(w[0][0]), "+v"(w[1][0]), "+v"(w[0][1]), "+v"(w[1][1]), "+v"(w[0][2]),
-                   "+v"(w[1][2]), "+v"(w[0][3]), "+v"(w[1][3]), "+v"(w[0][4]), "+v"(w[1][4]),
-                   "+v"(w[0][5]), "+v"(w[1][5]), "+v"(w[0][6]), "+v"(w[1][6]), "+v"(w[0][7]),
-                   "+v"(w[1][7]));
-  } else {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(w[0][0]), "+v"(w[1][0]), "+v"(w[0][1]), "+v"(w[1][1]), "+v"(w[0][2]),
-                   "+v"(w[1][2]), "+v"(w[0][3]), "+v"(w[1][3]));
-  }
-#pragma unroll
-  for (int db = 0; db < G::DB; ++db) {
-    const u32x4_t vf = {w[0][db][0], w[0][db][1], w[1][db][0], w[1][db][1]};
-    acc[db] = mfma_16x16x32(vf, pk, acc[db]);
-  }
+  VFrags<D> v;
+  pv_issue<D>(vbase, v, lane);
+  pv_finish<D>(v, pk, acc);
 }
 
 // The verify tokens' own keys and values and the mask among them (target verification:
@@ -1662,27 +1735,23 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
 
 // Small calls: a few units split over many shares (one sequence at batch 1, a handful at
 // most), whose whole K/V fits one pass of workgroups over the CUs. One workgroup per share
-// of at most SMALL_TILES tiles, W consumer wavefronts (one per 16-row block of the unit),
-// no producer and no ring: the share's page ids, then all of its K/V loads are issued at
-// once into stages of their own (the persistent kernel's stage layout), the first
-// segment's query rows are loaded (the caller's rows with the prologue applied by the
-// query pass's code, or the packed rows) while the tiles fly, and the tiles are computed
-// in order. The same line of tiles, shares and partial slots as attn_fwd_kernel, so the
-// combine merges the partials unchanged. A share of several units loads each further
-// unit's query rows at its segment start.
+// of at most SMALL_TILES tiles (the host sizes shares to about one per CU), W consumer
+// wavefronts (one per 16-row block of the unit) and one loader wavefront, no ring: the
+// loader issues the share's page ids, then every K/V load of the share at once into
+// stages of their own (the persistent kernel's stage layout), and publishes each tile
+// with a barrier as its loads complete. The consumers meanwhile load the first segment's
+// query rows and apply the prologue (their own memory queue, so its dependent loads --
+// positions, then rotary rows -- are not ordered behind the K/V stream), then compute the
+// tiles in order. A share of several units loads each further unit's query rows at its
+// segment start. The same line of tiles, shares and partial slots as attn_fwd_kernel;
+// attn_merge_wide_kernel merges the partials.
 constexpr int SMALL_TILES = 8;  // stages per workgroup: 8 x 17.2 KB of LDS at head_dim 128
 
 template <int D>
 __device__ __forceinline__ void small_query_rows(const AttnArgs &a, int64_t unit, int r, int g,
-                                                 u32x4_t (&qf)[D / 32], bool direct) {
+                                                 u32x4_t (&qf)[D / 32]) {
   constexpr int KT = D / 32;
   typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
-  if (!direct) {  // packed by the query pass (prologue applied, invalid rows zero)
-    const uint16_t *src = a.qp + (unit * 16 * a.nrb + r) * D + 8 * g;
-#pragma unroll
-    for (int t = 0; t < KT; ++t) qf[t] = *(g_u32x4_t *)(src + 32 * t);
-    return;
-  }
   const int b = (int)(unit / a.ups);
   const int ul = (int)(unit - (int64_t)b * a.ups);
   const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
@@ -1704,12 +1773,12 @@ __device__ __forceinline__ void small_query_rows(const AttnArgs &a, int64_t unit
     if (!valid) qf[t] = u32x4_t{0, 0, 0, 0};
 }
 
-template <int LAYOUT, int W, int D, bool DIRECT>
-__global__ __launch_bounds__(64 * W) void attn_small_kernel(const AttnArgs a, const int32_t *__restrict__ table,
-                                                            const int32_t *__restrict__ plan,
-                                                            const int32_t *__restrict__ seqlens) {
+template <int LAYOUT, int W, int D>
+__global__ __launch_bounds__(64 * (W + 1)) void attn_small_kernel(const AttnArgs a,
+                                                                  const int32_t *__restrict__ table,
+                                                                  const int32_t *__restrict__ plan,
+                                                                  const int32_t *__restrict__ seqlens) {
   using G = Geo<D>;
-  constexpr int KPW = (G::NI + W - 1) / W;  // this wavefront's loads per tile
   constexpr bool IDS = LAYOUT != CONTIG;
   __shared__ __attribute__((aligned(1024))) char stages[SMALL_TILES * G::STAGE];
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -1722,46 +1791,57 @@ __global__ __launch_bounds__(64 * W) void attn_small_kernel(const AttnArgs a, co
   if (ntiles <= 0) return;  // uniform over the workgroup
   auto stage = [&](int t) { return stages + (t % SMALL_TILES) * G::STAGE; };
   Cursor cc = cursor_at(a, sm, T0);
-  Cursor ct = cc;  // paged layouts: the next tile whose page ids are loaded
-  Loader ld;       // the next tile whose K/V are loaded
-  ld.c = cc;
-  loader_unit<LAYOUT>(a, ld);
-  uint32_t loff[KPW];
+  // Both roles take the same barriers: per chunk of SMALL_TILES tiles (a share longer than
+  // that only with lengths past max_seqlen_k), one before its stages are reloaded (not
+  // for the first) and one per tile as it lands.
+  if (wave == W) {  // ---------------------------------------------------------- loader
+    uint32_t loff[G::NI];  // byte offsets inside a 16-position block of this lane's loads
 #pragma unroll
-  for (int k = 0; k < KPW; ++k) {
-    int row, coff, dst;
-    bool isk;
-    const int i = wave + k * W;
-    load_slot<D>(i < G::NI ? i : 0, lane, row, coff, isk, dst);
-    loff[k] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + (uint32_t)coff;
+    for (int i = 0; i < G::NI; ++i) {
+      int row, coff, dst;
+      bool isk;
+      load_slot<D>(i, lane, row, coff, isk, dst);
+      loff[i] = (uint32_t)(row & 15) * (isk ? a.k_tok_b : a.v_tok_b) + (uint32_t)coff;
+    }
+    Cursor ct = cc;  // paged layouts: the next tile whose page ids are loaded
+    Loader ld;       // the next tile whose K/V are loaded
+    ld.c = cc;
+    loader_unit<LAYOUT>(a, ld);
+    for (int c0 = 0; c0 < ntiles; c0 += SMALL_TILES) {
+      const int c1 = ntiles - c0 < SMALL_TILES ? ntiles : c0 + SMALL_TILES;
+      if (c0 > 0) block_sync();  // the consumers are done with the stages being reloaded
+      if (IDS) {  // the chunk's page ids, which the K/V loads below read from LDS
+        for (int j = c0; j < c1; ++j) {
+          issue_ids<LAYOUT, D>(a, table, ct, stage(j), lane);
+          if (j + 1 < ntiles) cursor_next(a, sm, ct);
+        }
+        wait_vm<0>();
+        asm volatile("" ::: "memory");  // the id reads stay after the wait
+      }
+      for (int j = c0; j < c1; ++j) {
+        issue_kv<LAYOUT, D, 1>(a, ld, stage(j), 0, lane, loff);
+        if (j + 1 < ntiles) loader_advance<LAYOUT>(a, sm, ld);
+      }
+      for (int j = c0; j < c1; ++j) {  // tile j lands: its loads and all before are complete
+        wait_vm((c1 - 1 - j) * G::NI);
+        block_sync();
+      }
+    }
+    return;
   }
+  // ---------------------------------------------------------------------- consumers
   const int r = wave * 16 + n;
   u32x4_t qf[G::KT];
+  small_query_rows<D>(a, cc.u, r, g, qf);  // while the loader's tiles fly
   f32x4_t acc[G::DB];
   float m = -INFINITY, l = 0.f;
-  // The host sizes shares to at most SMALL_TILES tiles (one chunk); a longer share (lengths
-  // past max_seqlen_k) is walked in chunks of SMALL_TILES stages.
   for (int c0 = 0; c0 < ntiles; c0 += SMALL_TILES) {
     const int c1 = ntiles - c0 < SMALL_TILES ? ntiles : c0 + SMALL_TILES;
-    if (c0 > 0) block_sync();  // every wavefront is done with the stages being reloaded
-    if (IDS) {  // the chunk's page ids: tile j's by wavefront j % W, awaited and published
-      for (int j = c0; j < c1; ++j) {
-        if (j % W == wave) issue_ids<LAYOUT, D>(a, table, ct, stage(j), lane);
-        if (j + 1 < ntiles) cursor_next(a, sm, ct);
-      }
-      wait_vm<0>();
-      block_sync();
-    }
-    for (int j = c0; j < c1; ++j) {  // every K/V load of the chunk: load i of a tile by wavefront i % W
-      issue_kv<LAYOUT, D, W>(a, ld, stage(j), wave, lane, loff);
-      if (j + 1 < ntiles) loader_advance<LAYOUT>(a, sm, ld);
-    }
-    if (c0 == 0) small_query_rows<D>(a, cc.u, r, g, qf, DIRECT);  // while the tiles fly
-    wait_vm<0>();
-    block_sync();
+    if (c0 > 0) block_sync();
     for (int i = c0; i < c1; ++i) {
+      block_sync();  // tile i has landed
       if (i == 0 || cc.lt == 0) {  // a segment starts: a fresh accumulator (rows of a further unit)
-        if (i > 0) small_query_rows<D>(a, cc.u, r, g, qf, DIRECT);
+        if (i > 0) small_query_rows<D>(a, cc.u, r, g, qf);
 #pragma unroll
         for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         m = -INFINITY;
@@ -1911,6 +1991,99 @@ __global__ __launch_bounds__(2 * D) void attn_combine_kernel(const AttnArgs a) {
              mg.acc);
 }
 
+// Merge for calls whose units are split over many shares (the small-call kernel: tens of
+// segments per unit). Eight lanes per (unit, row, 8-channel chunk): lane j takes segments
+// j, j + 8, ..., WIDE_MB of them per batch with all of the batch's loads issued before
+// any is used, so up to 8 WIDE_MB segments cost one memory round trip; the eight running
+// merges then combine over a butterfly. attn_combine_kernel's one thread per chunk
+// walks the segments itself, which at 16-32 segments is several round trips and 16-32
+// partial rows read by each of a few workgroups per unit.
+constexpr int WIDE_LANES = 8;
+constexpr int WIDE_MB = 4;
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_merge_wide_kernel(const AttnArgs a) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+  constexpr int C = D / 8;  // 8-channel chunks per row
+  const int rows = a.nrb * 16;
+  const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) / WIDE_LANES;
+  const int j = (int)threadIdx.x % WIDE_LANES;
+  const int64_t units = (int64_t)a.batch * a.ups;
+  if (item >= units * rows * C) return;  // whole groups of eight lanes
+  const int64_t unit = item / (rows * C);
+  const int rc = (int)(item - unit * rows * C);
+  const int r = rc / C, c = rc - r * C;
+  const int b = (int)(unit / a.ups);
+  const int ul = (int)(unit - (int64_t)b * a.ups);
+  const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
+  const int R = rg * rows + r;
+  const int gq = R / a.q_len, tq = R - gq * a.q_len;
+  if (gq >= a.group || tq >= q_rows_of(a, b)) return;  // the group's row is not a draft row
+  const float vs = a.vd ? a.v_scale * a.vd[(int64_t)b * a.d_sb + (int64_t)h * a.d_sh] : a.v_scale;
+  RowMerge mg;
+  const int64_t pre = tile_prefix(a, a.plan, b);
+  const int tiles_b = (int)(tile_prefix(a, a.plan, b + 1) - pre);
+  if (tiles_b > 0) {
+    const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
+    const int64_t nw = a.num_shares;
+    const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
+    const int64_t wa = share_of(U0, total, nw);
+    const int nseg = (int)(share_of(U0 + tiles_b - 1, total, nw) - wa) + 1;
+    const bool sparse = nw > total;  // empty shares write nothing: their slots are skipped
+    for (int s0 = j; s0 < nseg; s0 += WIDE_LANES * WIDE_MB) {
+      f32x2_t ls[WIDE_MB];
+      u32x4_t ow[WIDE_MB];
+#pragma unroll
+      for (int k = 0; k < WIDE_MB; ++k) {
+        const int s = s0 + k * WIDE_LANES;
+        const int64_t w = wa + s;
+        const bool in = s < nseg && (!sparse || share_start(w + 1, total, nw) > share_start(w, total, nw));
+        const int64_t row = (unit + w) * rows + r;
+        ls[k] = in ? *reinterpret_cast<const f32x2_t *>(a.part_lse + 2 * row) : f32x2_t{-INFINITY, 1.f};
+        ow[k] = in ? load16(a.part_o + row * D + 8 * c) : u32x4_t{0, 0, 0, 0};
+      }
+      float Mb = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < WIDE_MB; ++k) Mb = fmaxf(Mb, ls[k][0]);
+      if (Mb == -INFINITY) continue;  // no segment of the batch saw a position
+      f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      float den = 0.f;
+#pragma unroll
+      for (int k = 0; k < WIDE_MB; ++k) {
+        const bool seen = ls[k][0] != -INFINITY;
+        const float f = seen ? __builtin_amdgcn_exp2f(ls[k][0] - Mb) : 0.f;
+        const float fx = f * (ls[k][1] * vs);
+        den += f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const f32x4_t x = {f16_lo(ow[k][2 * e]), f16_hi(ow[k][2 * e]), f16_lo(ow[k][2 * e + 1]),
+                             f16_hi(ow[k][2 * e + 1])};
+          if (seen) acc[e] += x * fx;
+        }
+      }
+      mg.add(Mb, 1.f, den, acc);
+    }
+  }
+  // Butterfly over the group's eight lanes (every lane of the group reaches it).
+#pragma unroll
+  for (int off = 1; off < WIDE_LANES; off <<= 1) {
+    const float Mo = __shfl_xor(mg.M, off, WIDE_LANES);
+    const float dn = __shfl_xor(mg.den, off, WIDE_LANES);
+    f32x4_t xo[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xo[e][q] = __shfl_xor(mg.acc[e][q], off, WIDE_LANES);
+    if (Mo != -INFINITY) mg.add(Mo, 1.f, dn, xo);
+  }
+  if (j != 0) return;
+  mg.finish();
+  const int64_t head = (int64_t)h * a.group + gq;
+  store_row8(a.o + (a.cu_q ? (q_token_index(a, b, 0) + tq) * a.o_st : (int64_t)b * a.o_sb + (int64_t)tq * a.o_st) +
+                 head * a.o_sh + 8 * c,
+             mg.acc);
+}
+
 // plan[0] = 0, plan[b + 1] = plan[b] + ceil(max(L_b, 0) / tile), L_b = seqlens[b], or
 // seqlens[b + 1] - seqlens[b] when seqlens is a CSR indptr (csr != 0).
 // The plan holds two tile prefixes, for bf16 K/V (TILE positions) at plan[0 .. batch] and
@@ -1987,10 +2160,10 @@ static int dq_seq_cap(int w) {
 template <int LAYOUT, int D>
 static AttnKernel pick_small(int w) {
   switch (w) {
-    case 2: return attn_small_kernel<LAYOUT, 2, D, true>;
-    case 4: return attn_small_kernel<LAYOUT, 4, D, true>;
-    case 5: return attn_small_kernel<LAYOUT, 5, D, true>;
-    case 8: return attn_small_kernel<LAYOUT, 8, D, true>;
+    case 2: return attn_small_kernel<LAYOUT, 2, D>;
+    case 4: return attn_small_kernel<LAYOUT, 4, D>;
+    case 5: return attn_small_kernel<LAYOUT, 5, D>;
+    case 8: return attn_small_kernel<LAYOUT, 8, D>;
     default: return nullptr;
   }
 }
@@ -2121,18 +2294,19 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
 // Tiles per share of attn_small_kernel for a bf16 call without verify tokens, or 0 where
 // the persistent kernel runs: the small kernel takes calls whose K/V fits one pass of
 // SMALL_TILES-tile workgroups over the CUs and whose row blocks per unit it has an
-// instance for. FLASHMAP_SMALL_TILES sets the tiles per share (1 .. SMALL_TILES, default
-// 4); 0 turns the kernel off.
+// instance for. Shares are sized to about one per CU (each CU's loads in flight bound
+// the stream; partials grow with the shares). FLASHMAP_SMALL_TILES sets the tiles per
+// share (1 .. SMALL_TILES) instead; 0 turns the kernel off.
 static int small_tiles_for(int layout, int batch, int q_len, int hq, int hkv, int d, int max_k) {
   DeviceInfo info;
   if (device_info(&info) != FM_OK) return 0;
   const RowPlan rp = row_plan(hq / hkv, q_len);
   const int64_t tiles_bound = (int64_t)hkv * rp.rgroups * batch * (((int64_t)max_k + TILE - 1) / TILE);
-  int tps = env_int("FLASHMAP_SMALL_TILES", 4);
+  if (tiles_bound > (int64_t)info.cus * SMALL_TILES || select_small(layout, d, rp.nrb) == nullptr) return 0;
+  int tps = (int)((tiles_bound + info.cus - 1) / info.cus);
+  tps = env_int("FLASHMAP_SMALL_TILES", tps);
   tps = tps > SMALL_TILES ? SMALL_TILES : tps;
-  if (tps <= 0 || tiles_bound > (int64_t)info.cus * SMALL_TILES || select_small(layout, d, rp.nrb) == nullptr)
-    return 0;
-  return tps;
+  return tps > 0 ? tps : 0;
 }
 
 static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -2306,7 +2480,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   if (qmode != Q_DIRECT) FM_CHECK_HIP(hipGetLastError());
   AttnKernel k = small_tiles > 0 ? select_small(layout, c.d, sz.rp.nrb) : select_kernel(layout, c.d, sz.rp.nrb, qmode);
-  const dim3 kblock(small_tiles > 0 ? 64 * sz.rp.nrb : 64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb));
+  const dim3 kblock(small_tiles > 0 ? 64 * (sz.rp.nrb + 1) : 64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb));
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
@@ -2314,6 +2488,17 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
                                           c.stream);
   profile_after(c.stream);
   if (lerr != hipSuccess) return fail(FM_ERR_HIP, "attention launch failed: %s", hipGetErrorString(lerr));
+  if (small_tiles > 0) {  // the wide merge: eight lanes per (unit, row, 8-channel chunk)
+    const int64_t lanes = units * sz.rp.nrb * 16 * (c.d / 8) * WIDE_LANES;
+    const int64_t mblocks = (lanes + 255) / 256;
+    FM_REQUIRE(mblocks < (1ll << 31), "too many units");
+    if (c.d == 128)
+      attn_merge_wide_kernel<128><<<dim3((unsigned)mblocks), dim3(256), 0, c.stream>>>(a);
+    else
+      attn_merge_wide_kernel<64><<<dim3((unsigned)mblocks), dim3(256), 0, c.stream>>>(a);
+    FM_CHECK_HIP(hipGetLastError());
+    return FM_OK;
+  }
   // One workgroup of 2 D threads per 16-row block; units split into many segments (a
   // call of few units over the whole grid) merge their partials 8 at a time.
   const int64_t cblocks = units * sz.rp.nrb;
