@@ -857,7 +857,7 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, con
   }
   uint16_t *dst = const_cast<uint16_t *>(a.qp) + (unit * 16 * a.nrb + r) * D + 8 * g;
 #pragma unroll
-  for (int t = 0; t < KT; ++t) store16(dst + 32 * t, valid ? qf[t] : u32x4_t{0, 0, 0, 0});
+  for (int t = 0; t < KT; ++t) store16_nt(dst + 32 * t, valid ? qf[t] : u32x4_t{0, 0, 0, 0});
   if constexpr (VERIFY) {
     using G = Geo<D>;
     __shared__ __attribute__((aligned(1024))) char vstage[4][G::VBLKS * G::VPITCH];
@@ -1946,7 +1946,7 @@ __device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, 
 }
 
 __device__ __forceinline__ void store_row8(uint16_t *dst, const f32x4_t (&acc)[2]) {
-  store16(dst, u32x4_t{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+  store16_nt(dst, u32x4_t{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
                        pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])});
 }
 
