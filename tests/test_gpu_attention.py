@@ -425,3 +425,23 @@ def test_small_call_kernel(dev, monkeypatch, layout, hq, hkv, lens):
                 continue
             want = ref.attention(qn[s:e].transpose(0, 1), k[i, :, : int(lens[i])], v[i, :, : int(lens[i])])
             check_close(got[s:e], want.transpose(0, 1))
+
+
+@pytest.mark.parametrize("tiles", ["", "1"])
+def test_small_call_fits_the_queried_workspace(dev, monkeypatch, tiles):
+    """fm_attn_workspace_bytes covers the small-call kernel at any tiles per share: a
+    workspace of exactly the queried size runs the same kernel and split as the pool's
+    larger one (identical bits), at C2's shape."""
+    g = gen(44)
+    b, hq, hkv, d, t, ctx = 1, 32, 8, 128, 16, 2048
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    k = normed_keys(b, hkv, ctx, d, g)
+    v = torch.randn(b, hkv, ctx, d, generator=g).bfloat16()
+    o = ops()
+    monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
+    pooled = o.block_attention_contig(q.to(dev), k.to(dev), v.to(dev))
+    monkeypatch.setattr(o._WORKSPACES, "get",
+                        lambda device, nbytes: torch.empty(nbytes, dtype=torch.uint8, device=device))
+    exact = o.block_attention_contig(q.to(dev), k.to(dev), v.to(dev))
+    assert torch.equal(pooled, exact), "the queried workspace must fit the small-call kernel"
+    check_close(exact, ref.block_attention_contig(q, k, v))
