@@ -445,3 +445,27 @@ def test_small_call_fits_the_queried_workspace(dev, monkeypatch, tiles):
     exact = o.block_attention_contig(q.to(dev), k.to(dev), v.to(dev))
     assert torch.equal(pooled, exact), "the queried workspace must fit the small-call kernel"
     check_close(exact, ref.block_attention_contig(q, k, v))
+
+
+@pytest.mark.parametrize("tiles", ["1", "0"])
+def test_lengths_past_max_seqlen_k(dev, monkeypatch, tiles):
+    """Lengths beyond ``max_seqlen_k`` (the caller's bound, used to size the split): the
+    shares then hold more tiles than planned (more than the small-call kernel's 8 stages,
+    so it walks them in chunks); the results still match the oracle. 0: the persistent
+    kernel."""
+    g = gen(45)
+    hq, hkv, d, t, page = 32, 8, 128, 16, 16
+    lens = torch.tensor([700, 300, 33])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
+    monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
+    got = ops().block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
+                                      t, 1, d ** -0.5)
+    check_close(got, want)
