@@ -24,9 +24,10 @@
 //   attn_fwd_kernel      the K/V stream and the online softmax
 //   attn_combine_kernel  the merge and the scatter into the caller's output layout
 // Small calls (the whole K/V within one pass of 8-tile workgroups over the CUs: batch 1
-// at a few thousand positions) run attn_small_kernel in place of the first two: one
-// workgroup per share of a few tiles, all of its loads issued at once, the caller's rows
-// read directly; the combine is the same.
+// at a few thousand positions) run attn_small_kernel in place of the first two (one
+// workgroup per share of about one CU's worth of tiles, a loader wavefront issuing all of
+// its loads at once, the caller's rows read directly) and attn_merge_wide_kernel in place
+// of the combine (eight lanes per output row chunk, for the tens of segments per unit).
 //
 // Workgroup = one wavefront per 16-row block of the unit (4 at GQA 4 x 16 rows). All
 // wavefronts walk the share's tiles together: K/V tiles stream from HBM straight into
