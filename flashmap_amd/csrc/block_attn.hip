@@ -674,6 +674,13 @@ __device__ __forceinline__ void pv_finish_f8(VFragsF8<D> &v, int h, const u32x4_
   }
 }
 
+// max(a, b, c) in one v_max3_f32, for operands known not to be NaN.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // One tile for this wavefront's 16 rows: S^T = K Q^T, online softmax, O^T += V^T P^T. sl:
 // this lane's row's score scale in log2 units (softmax_scale log2(e), times the row's
 // query and key descales with fp8 K/V). F8: K and Q are e4m3 (the fp8 MFMA, each 16-byte
@@ -761,9 +768,13 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
       for (int i = 0; i < 4; ++i)
         if (pos0 + 16 * pb + 4 * g + i >= L) s[pb][i] = -INFINITY;
   }
-  float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+  // The lane's row max with three-input maxima: fmaxf makes the compiler quiet each MFMA
+  // result first (an extra max per value); the scores are never NaN here (finite products,
+  // -inf where masked).
+  float mx = max3f(s[0][0], s[0][1], s[0][2]);
 #pragma unroll
-  for (int pb = 1; pb < NH; ++pb) mx = fmaxf(mx, fmaxf(fmaxf(s[pb][0], s[pb][1]), fmaxf(s[pb][2], s[pb][3])));
+  for (int k = 3; k + 1 < 4 * NH; k += 2) mx = max3f(mx, s[k / 4][k % 4], s[(k + 1) / 4][(k + 1) % 4]);
+  mx = max3f(mx, s[NH - 1][3], s[NH - 1][3]);  // 4 NH - 3 values after the first three: an odd count
   mx = max_over_groups(mx) * sl;
   // Lazy rescale: the reference max m moves only when a row's tile max exceeds it by
   // more than 8 (log2 units), so P <= 2^8 in between and O^T/l are rescaled rarely. This
