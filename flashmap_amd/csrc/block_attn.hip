@@ -114,6 +114,7 @@ struct AttnArgs {
   int32_t batch, hkv, rgroups, ups;  // ups = hkv * rgroups units per sequence
   int32_t nrb;                       // 16-row blocks (wavefronts) per unit
   int32_t num_shares;  // workgroups x replicas
+  int32_t share_c;     // a unit's extra cost in tiles when the line is cut into shares (share_first_tiles)
   float scale_log2;
   float v_scale;  // combine: scale of the context partials' values (1 but for verify calls)
   int32_t tail;   // verify calls: unit u's verify-token partial is slot units + num_shares + u
@@ -273,6 +274,11 @@ struct SeqMeta {
     if (!var()) return (int64_t)b * a.uniform_tiles;
     return staged ? (int64_t)tab[b][0] : (int64_t)sload(plan + b);
   }
+  // The same with b differing between lanes (a vector load when not staged).
+  __device__ __forceinline__ int64_t prefix_lane(const AttnArgs &a, int b) const {
+    if (!var()) return (int64_t)b * a.uniform_tiles;
+    return staged ? (int64_t)tab[b][0] : (int64_t)plan[b];
+  }
   // tiles(b) = prefix(b + 1) - prefix(b), the length of sequence b and the offset of
   // its page ids. CSR: the second array is indptr, so the length is a difference.
   __device__ __forceinline__ void seq(const AttnArgs &a, int b, int &tiles, int &L, int64_t &row) const {
@@ -353,6 +359,59 @@ __device__ __forceinline__ Cursor cursor_at(const AttnArgs &a, const SeqMeta<VAR
   c.rg = ul - c.h * a.rgroups;
   c.u = lo * a.ups + ul;
   return c;
+}
+
+// Shares are cut by cost, not by tiles: every unit counts its tiles plus a.share_c, the
+// measured overhead of a segment (taking the next unit's query rows, handing a partial
+// over) in tiles, so that shares holding many short units get fewer tiles. The cost line
+// follows the tile line: sequence b's units start at cost ups (prefix(b) + c b), each
+// spans tiles_b + c, its tile t at c + t. share_c = 0 gives the tile line itself.
+//
+// F[k] = first tile (index on the tile line) of share s0 + k; a share at or past
+// num_shares gives the line's end. Every lane takes one sequence per pass (one LDS read
+// each when the metadata is staged), and a ballot per boundary counts the sequences whose
+// cost start lies at or before it.
+template <int NB, bool VAR>
+__device__ __forceinline__ void share_first_tiles(const AttnArgs &a, const SeqMeta<VAR> &sm, int64_t s0,
+                                                  int64_t (&F)[NB]) {
+  const int64_t c = a.share_c;
+  const int64_t end = (int64_t)a.ups * sm.prefix(a, a.batch);  // the tile line's end
+  const int64_t total = end + (int64_t)a.ups * c * a.batch;     // the cost line's end
+  int64_t P[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) P[k] = share_start(s0 + k, total, a.num_shares);
+  if (c == 0) {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) F[k] = P[k];
+    return;
+  }
+  int cnt[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) cnt[k] = 0;
+  const int lane = threadIdx.x & 63;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    const bool ok = b < a.batch;
+    const int64_t cb = (int64_t)a.ups * ((ok ? sm.prefix_lane(a, b) : 0) + c * b);
+#pragma unroll
+    for (int k = 0; k < NB; ++k) cnt[k] += __popcll(__builtin_amdgcn_ballot_w64(ok && cb <= P[k]));
+  }
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const int lo = cnt[k] - 1;  // the last sequence whose cost start is <= P (cost(0) = 0)
+    const int64_t pre = sm.prefix(a, lo);
+    const int64_t tb = sm.prefix(a, lo + 1) - pre;
+    const int64_t off = P[k] - (int64_t)a.ups * (pre + c * lo);  // < ups (tb + c)
+    const int64_t span = tb + c;
+    int64_t ul;
+    if ((off >> 31) == 0)  // the usual case: a 32-bit division
+      ul = (int64_t)((uint32_t)off / (uint32_t)span);
+    else
+      ul = off / span;
+    const int64_t pos = off - ul * span;
+    const int64_t t = (int64_t)a.ups * pre + ul * tb + (pos >= c ? pos - c : 0);  // in the overhead: tile 0
+    F[k] = s0 + k >= a.num_shares ? end : t;
+  }
 }
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -1482,18 +1541,19 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   const int n = lane & 15, g = lane >> 4;
   char *const smem = smem_all + rep * RBYTES;
   char *const out = smem + G::SMEM;
-  const int64_t total = (int64_t)a.ups * sm.prefix(a, a.batch);
   const int share = (int)blockIdx.x * R + rep;
-  const int64_t T0 = share_start(share, total, a.num_shares);
-  const int ntiles = (int)(share_start(share + 1, total, a.num_shares) - T0);
+  int64_t F[R + 1];  // first tiles of the workgroup's shares and the next one
+  share_first_tiles(a, sm, (int64_t)blockIdx.x * R, F);
+  int64_t T0 = F[0];
+  int ntiles = 0;
   // Iterations of the workgroup: the largest share among its replicas (every wavefront
   // takes part in every barrier; a replica past its share only waits at them).
   int nloop = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t sr = (int64_t)blockIdx.x * R + r;
-    const int nr = (int)(share_start(sr + 1, total, a.num_shares) - share_start(sr, total, a.num_shares));
+    const int nr = (int)(F[r + 1] - F[r]);
     nloop = nr > nloop ? nr : nloop;
+    if (r == rep) T0 = F[r], ntiles = nr;
   }
   Cursor cc = Cursor{0, 0, 0, 0, 0, 0, 0, 0};  // tile being computed (i)
   if (ntiles > 0) cc = cursor_at(a, sm, T0);
@@ -1796,10 +1856,11 @@ __global__ __launch_bounds__(64 * (W + 1)) void attn_small_kernel(const AttnArgs
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, g = lane >> 4;
   SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens, nullptr, false};
-  const int64_t total = (int64_t)a.ups * sm.prefix(a, a.batch);
   const int share = (int)blockIdx.x;
-  const int64_t T0 = share_start(share, total, a.num_shares);
-  const int ntiles = (int)(share_start(share + 1, total, a.num_shares) - T0);
+  int64_t F[2];
+  share_first_tiles(a, sm, (int64_t)share, F);
+  const int64_t T0 = F[0];
+  const int ntiles = (int)(F[1] - F[0]);
   if (ntiles <= 0) return;  // uniform over the workgroup
   auto stage = [&](int t) { return stages + (t % SMALL_TILES) * G::STAGE; };
   Cursor cc = cursor_at(a, sm, T0);
@@ -1912,9 +1973,10 @@ __device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, 
   const int64_t pre = tile_prefix(a, a.plan, b);
   const int tiles_b = (int)(tile_prefix(a, a.plan, b + 1) - pre);
   if (tiles_b <= 0) return;
-  const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
+  const int64_t uc = a.share_c;  // a unit's extra cost on the line (share_first_tiles)
+  const int64_t total = (int64_t)a.ups * (tile_prefix(a, a.plan, a.batch) + uc * a.batch);  // the cost line
   const int64_t nw = a.num_shares;
-  const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
+  const int64_t U0 = (int64_t)a.ups * (pre + uc * b) + (int64_t)ul * (tiles_b + uc) + uc;  // cost of tile 0
   const int64_t wa = share_of(U0, total, nw);
   const int nseg = (int)(share_of(U0 + tiles_b - 1, total, nw) - wa) + 1;
   const int64_t row0 = (unit + wa) * rows + r;
@@ -2036,9 +2098,10 @@ __global__ __launch_bounds__(256) void attn_merge_wide_kernel(const AttnArgs a) 
   const int64_t pre = tile_prefix(a, a.plan, b);
   const int tiles_b = (int)(tile_prefix(a, a.plan, b + 1) - pre);
   if (tiles_b > 0) {
-    const int64_t total = (int64_t)a.ups * tile_prefix(a, a.plan, a.batch);
+    const int64_t uc = a.share_c;  // a unit's extra cost on the line (share_first_tiles)
+    const int64_t total = (int64_t)a.ups * (tile_prefix(a, a.plan, a.batch) + uc * a.batch);  // the cost line
     const int64_t nw = a.num_shares;
-    const int64_t U0 = (int64_t)a.ups * pre + (int64_t)ul * tiles_b;
+    const int64_t U0 = (int64_t)a.ups * (pre + uc * b) + (int64_t)ul * (tiles_b + uc) + uc;  // cost of tile 0
     const int64_t wa = share_of(U0, total, nw);
     const int nseg = (int)(share_of(U0 + tiles_b - 1, total, nw) - wa) + 1;
     const bool sparse = nw > total;  // empty shares write nothing: their slots are skipped
@@ -2402,7 +2465,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     // forces the pass, =0 the direct rows where they apply; both give the same bits.
     const int force = env_int("FLASHMAP_QUERY_PASS", -1);
     const int64_t units = (int64_t)c.batch * c.hkv * rp.rgroups;
-    const bool small = units * 2 <= sz.num_shares;
+    const bool small = units <= sz.num_shares;
     if (fast_rope && c.batch <= cap && (force == 0 || (force < 0 && small))) qmode = Q_DIRECT;
   }
   // Small calls: attn_small_kernel with the caller's rows read directly (two launches),
@@ -2453,6 +2516,16 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   a.q_pos = c.q_pos;
   a.eps = c.eps;
   a.num_shares = sz.num_shares;
+  // A unit's extra cost when cutting the line into shares (share_first_tiles), in tiles:
+  // what a segment start and a partial hand-off cost the persistent kernel, measured best
+  // at 2 tiles for bf16 (32 positions) and 4 for e4m3 (64 positions). Where the units span
+  // more than four shares each on average, every share holds one or two segments whatever
+  // the cut, and an extra cost only unbalances shares of equal units (C4's 32768-position
+  // sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
+  // FLASHMAP_SHARE_COST overrides.
+  const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares ? (a.f8 ? 4 : qmode == Q_DIRECT ? 6 : 2) : 0;
+  a.share_c = small_tiles > 0 ? 0 : env_int("FLASHMAP_SHARE_COST", share_c);
+  if (a.share_c < 0) a.share_c = 0;
   a.tail = vf != nullptr;
   if (!a.tail) a.v_scale = 1.f;
   char *ws = (char *)c.ws;

@@ -363,6 +363,7 @@ def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
                                             seqlens_k=lens.to(dev), prologue=pro)
     outs = {}
     monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")  # the persistent kernel (the small-call one reads rows directly)
+    monkeypatch.setenv("FLASHMAP_SHARE_COST", "2")  # one cut of the line for both (their default costs differ)
     for mode in ("1", "0"):
         monkeypatch.setenv("FLASHMAP_QUERY_PASS", mode)
         outs[mode] = run()
@@ -468,4 +469,37 @@ def test_lengths_past_max_seqlen_k(dev, monkeypatch, tiles):
     monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
     got = ops().block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
                                       t, 1, d ** -0.5)
+    check_close(got, want)
+
+
+@pytest.mark.parametrize("qpass", ["1", "0"])
+@pytest.mark.parametrize("cost", ["0", "1", "3", "6", "40"])
+def test_share_cost_cuts(dev, monkeypatch, cost, qpass):
+    """The persistent kernel cuts its line of tiles into shares by cost (every unit counts
+    its tiles plus a fixed cost): at any cost, including one that outweighs the tiles,
+    every tile is computed once and every partial merged, for sequences of 0 to 2000
+    positions, through the query pass (1) and with direct rows (0)."""
+    g = gen(47)
+    hq, hkv, d, t, page = 32, 8, 128, 16, 16
+    lens = torch.tensor([0, 5, 33, 700, 1, 64, 2000, 31, 0, 129, 16, 450])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(lmax + t + 1, d, 1e6)
+    pos = torch.cat([int(n) + torch.arange(t) for n in lens])
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    qn = ref.rms_norm_rope_vllm(q, w, table, pos, 1e-6)
+    want = ref.block_attention_paged_vllm(qn, cache, cu, lens, bt)
+    o = ops()
+    pro = o.Prologue(w.to(dev), o.rope_from_table(table.to(dev)), pos.to(dev), 1e-6)
+    monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")
+    monkeypatch.setenv("FLASHMAP_SHARE_COST", cost)
+    monkeypatch.setenv("FLASHMAP_QUERY_PASS", qpass)
+    got = o.block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
+                                  t, lmax, d ** -0.5, prologue=pro)
     check_close(got, want)
