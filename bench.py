@@ -99,6 +99,18 @@ def mfma_record(workload: str, flops: float, kernel_ms: float, fp8: bool) -> dic
     return rec
 
 
+def prologue_label(fp8: bool) -> str:
+    """Where the paged drafter workloads' QK-RMSNorm + RoPE runs. e4m3 calls quantize the
+    rows per head in a query pass; bf16 calls of at most one unit per share (the batch-64
+    workloads: 512 units over 512 shares) read the caller's rows in the attention kernel
+    unless FLASHMAP_QUERY_PASS=1 forces the pass."""
+    if fp8:
+        return "QK-RMSNorm + RoPE and the per-head e4m3 quantization in the call's query pass (its own launch)"
+    if os.environ.get("FLASHMAP_QUERY_PASS") == "1":
+        return "QK-RMSNorm + RoPE applied by the call's query pass (its own launch; FLASHMAP_QUERY_PASS=1)"
+    return "QK-RMSNorm + RoPE applied inside the attention kernel to the caller's rows (no query pass: two launches)"
+
+
 def algorithmic_bytes(inp, kv_bytes: int = 2) -> dict:
     lens, d, hq, hkv, k_rows, batch, page = (inp[k] for k in ("lens", "d", "hq", "hkv", "k_rows", "batch", "page"))
     sum_l = int(lens.sum())
@@ -961,7 +973,7 @@ def main() -> int:
             "ctx_lo": inp["lo"], "ctx_hi": inp["hi"], "ctx_sum": ab["sum_l"], "page": page,
             "layout": "vllm paged (blocks, kv_heads, page, 2*head_dim)" + (
                 f", virtual context-cache layout: caches of {virtual[1]} heads, runs {runs}" if virtual else ""),
-            "prologue": "QK-RMSNorm + RoPE applied by the call's query pass (its own launch)",
+            "prologue": prologue_label(fp8),
             "kv_dtype": "e4m3" if fp8 else "bf16",
         },
         "hbm_tbs": round(ab["total"] / (ms * 1e-3) / 1e12, 3),
