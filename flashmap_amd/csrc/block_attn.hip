@@ -5,17 +5,18 @@
 // row group rg): the G query heads sharing KV head h times the q_len draft rows,
 // packed into 16-row MFMA blocks (row r = query head h*G + r / q_len at token
 // r % q_len, the GQA row convention of flashmap/sglang/verify_attention.py:77-79).
-// Each unit's context is cut into tiles of 32 positions; all units' tiles form one
-// line (sequence-major, then head, then row group) that is cut into num_shares equal
-// shares, R per workgroup of the persistent grid (see replicas()). A share is walked
-// unit by unit, one "segment" per unit it touches, leaving for every segment one fp32
-// partial (O normalized by its own softmax sum, and the log-sum-exp) in slot
-// unit + share, which is unique along the line. attn_combine_kernel merges each
-// unit's partials (the LSE merge of flashmap/sglang/verify_attention.py:184-233) and
-// writes the bf16 output.
+// Each unit's context is cut into tiles of 32 positions (64 for e4m3 K/V); all units'
+// tiles form one line (sequence-major, then head, then row group) that is cut into
+// num_shares shares of equal cost (every unit counting its tiles plus a fixed cost for
+// its segment start, share_first_tiles), R per workgroup of the persistent grid (see
+// replicas()). A share is walked unit by unit, one "segment" per unit it touches,
+// leaving for every segment one partial (O normalized by its own softmax sum, in fp16
+// with a row scale, and the log2-sum-exp) in slot unit + share, which is unique along
+// the line. attn_combine_kernel merges each unit's partials (the LSE merge of
+// flashmap/sglang/verify_attention.py:184-233) and writes the bf16 output.
 //
-// Three launches per call (two when the units are at most half the shares: the
-// streaming kernel then reads the caller's query rows and applies the prologue itself):
+// Three launches per call (two when the units are at most the shares: the streaming
+// kernel then reads the caller's query rows and applies the prologue itself):
 //   pack_queries_kernel  the query rows of every unit, in the order the MFMA blocks
 //                        consume them, with the optional QK-RMSNorm + RoPE prologue
 //                        applied (invalid rows are zero): the streaming kernel then
@@ -29,13 +30,13 @@
 // its loads at once, the caller's rows read directly) and attn_merge_wide_kernel in place
 // of the combine (eight lanes per output row chunk, for the tens of segments per unit).
 //
-// Workgroup = one wavefront per 16-row block of the unit (4 at GQA 4 x 16 rows). All
-// wavefronts walk the share's tiles together: K/V tiles stream from HBM straight into
-// an LDS ring of STAGES tiles with LDS-DMA (global_load_lds_dwordx4, no registers in
-// flight), each wavefront issuing an equal part of every tile's 16-byte loads; tile i
-// is consumed after a hand-counted s_waitcnt vmcnt and a barrier while tiles
+// Replica of the persistent kernel = one producer wavefront and one consumer wavefront
+// per 16-row block of the unit (4 at GQA 4 x 16 rows). The producer streams the share's
+// K/V tiles from HBM straight into an LDS ring of STAGES tiles with LDS-DMA
+// (global_load_lds_dwordx4, no registers in flight) and stores the segments' partials;
+// tile i is consumed after its hand-counted s_waitcnt vmcnt and a barrier while tiles
 // i+1 .. i+STAGES-1 are in flight. K lands in LDS already in MFMA operand order. The
-// query rows of the next unit are loaded with the first tile of that unit, so a unit
+// consumers load the next unit's query rows while the current unit streams, so a unit
 // change costs no pipeline drain.
 // Per tile, wavefront w (its 16 rows r):
 //   S^T[pos][r] = K Q^T       v_mfma_f32_16x16x32_bf16, A = K from LDS, B = Q in registers
@@ -2458,11 +2459,12 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
                                                  c.rope_rs % 4 == 0 && ((uintptr_t)c.qn_w & 3) == 0);
     const int cap = c.d == 128 ? dq_seq_cap<128>(rp.nrb) : dq_seq_cap<64>(rp.nrb);
     // Direct rows cost a prologue at every segment start, inside the workgroup's barrier
-    // cycle (about 1.5 us per segment measured at 64 rows x D 128); the query pass costs a
-    // launch and one read + write of the rows. Direct wins when every share holds about one
-    // segment: units <= shares / 2 (a batch-1 call), and loses on full batches (C3's 512
-    // units over 512 shares: 184 us kernel against 165 + 8.5 us). FLASHMAP_QUERY_PASS=1
-    // forces the pass, =0 the direct rows where they apply; both give the same bits.
+    // cycle (about 5000 shader cycles at 64 rows x D 128), which the cost cut of the line
+    // absorbs (6 tiles per unit); the query pass costs a launch and one read + write of the
+    // rows. Measured: direct rows win up to one unit per share (C3's 512 units over 512
+    // shares: 176 us per call against 179 us with the pass); calls of more units than
+    // shares keep the pass. FLASHMAP_QUERY_PASS=1 forces the pass, =0 the direct rows where
+    // they apply; at one share cost both give the same bits.
     const int force = env_int("FLASHMAP_QUERY_PASS", -1);
     const int64_t units = (int64_t)c.batch * c.hkv * rp.rgroups;
     const bool small = units <= sz.num_shares;
