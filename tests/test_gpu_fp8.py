@@ -186,3 +186,25 @@ def test_paged_fp8_large_batch(dev):
     torch.cuda.synchronize()
     check_close(got.cpu().float(), ref.block_attention_paged_vllm_fp8(q8, cache, cu, lens, bt, d ** -0.5))
 
+
+
+@pytest.mark.parametrize("cost", ["0", "1", "4", "40"])
+def test_paged_fp8_share_cost_cuts(dev, monkeypatch, cost):
+    """The e4m3 kernel's line of 64-position tiles cut into shares by cost at any per-unit
+    cost (0: by tiles; 40: the cost outweighs the tiles): every tile computed once and
+    every partial merged, for sequences of 0 to 3000 positions."""
+    print(f"fp8 share cost {cost}", flush=True)
+    g = gen(97)
+    hq, hkv, d, page, k_rows = 32, 8, 128, 16, 16
+    lens = torch.tensor([0, 5, 65, 700, 1, 128, 3000, 63, 0, 129, 16, 450])
+    bs = len(lens)
+    bt, total = paged_layout(lens.tolist(), page, g)
+    cache = _e4m3((total, hkv, page, 2 * d), g)
+    q8 = _e4m3((bs * k_rows, hq, d), g)
+    cu = torch.arange(0, bs * k_rows + 1, k_rows, dtype=torch.int32)
+    desc = torch.rand(3, bs, hkv, generator=g) + 0.25
+    monkeypatch.setenv("FLASHMAP_SHARE_COST", cost)
+    got = ops().block_attention_paged_fp8(q8.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
+                                          k_rows, 3000, d ** -0.5, descales=desc.to(dev))
+    torch.cuda.synchronize()
+    check_close(got.cpu().float(), ref.block_attention_paged_vllm_fp8(q8, cache, cu, lens, bt, d ** -0.5, desc))
