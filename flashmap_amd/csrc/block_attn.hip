@@ -1503,32 +1503,50 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   SeqMeta<LAYOUT != CONTIG> sm{plan, seqlens, (lds_i32x2_t *)seq_tab, false};
   const bool stage_seq = sm.var() && a.batch <= SEQ;
   if (stage_seq || DQ) {  // uniform: every wavefront takes the barrier (DQ calls have batch <= SEQ)
-    // Every load of a thread's entries issued before any is used: the staging costs one
-    // round trip to memory, two with explicit query positions (token row, then position).
+    // Every load of a thread's entries issued before any is used, two entries per pass
+    // (a DQ call's batch x QTOK rotary rows take two passes of the workgroup at batch 64):
+    // the staging costs one round trip to memory per pass, two with explicit query
+    // positions (token row, then position).
     const bool pro = DQ && a.qn_w != nullptr;
-    for (int j = threadIdx.x; j <= a.batch || (pro && (j < a.batch * QTOK || j < D)); j += blockDim.x) {
-      int32_t p0 = 0, len = 0, c0 = j * a.q_len, c1 = (j + 1) * a.q_len, b0 = 0, b1 = 0;
-      float wj = 0.f;
-      const int bb = j / QTOK, tt = j - (j / QTOK) * QTOK;
-      if (stage_seq && j <= a.batch) p0 = plan[j], len = j < a.batch || a.csr ? seqlens[j] : 0;  // CSR: indptr[j]
-      if (DQ && j < a.batch && a.cu_q) c0 = a.cu_q[j], c1 = a.cu_q[j + 1];
-      if (pro && j < D) wj = a.qn_w[j];
-      if (pro && j < a.batch * QTOK) {
-        b0 = a.cu_q ? a.cu_q[bb] : bb * a.q_len;
-        b1 = a.cu_q ? a.cu_q[bb + 1] : (bb + 1) * a.q_len;
-      }
-      if (stage_seq && j <= a.batch) seq_tab[j] = i32x2_t{p0, len};
-      if constexpr (DQ) {
-        if (j < a.batch) {
-          int32_t rows = c1 - c0;
-          rows = rows < 0 ? 0 : (rows > a.q_len ? a.q_len : rows);
-          qmeta[j] = i32x2_t{c0, rows};
-        }
-        if (pro && j < D) w_tab[j] = wj;
+    auto wanted = [&](int j) { return j <= a.batch || (pro && (j < a.batch * QTOK || j < D)); };
+    constexpr int NJ = 2;
+    for (int j0 = threadIdx.x; wanted(j0); j0 += NJ * blockDim.x) {
+      int32_t p0[NJ], len[NJ], c0[NJ], c1[NJ], b0[NJ], b1[NJ];
+      float wj[NJ];
+#pragma unroll
+      for (int k = 0; k < NJ; ++k) {
+        const int j = j0 + k * (int)blockDim.x;
+        const int bb = j / QTOK;
+        p0[k] = 0, len[k] = 0, c0[k] = j * a.q_len, c1[k] = (j + 1) * a.q_len, b0[k] = 0, b1[k] = 0, wj[k] = 0.f;
+        if (stage_seq && j <= a.batch) p0[k] = plan[j], len[k] = j < a.batch || a.csr ? seqlens[j] : 0;  // CSR: indptr[j]
+        if (DQ && j < a.batch && a.cu_q) c0[k] = a.cu_q[j], c1[k] = a.cu_q[j + 1];
+        if (pro && j < D) wj[k] = a.qn_w[j];
         if (pro && j < a.batch * QTOK) {
-          const int64_t tok = (int64_t)b0 + tt;
-          const int64_t pos = tt >= b1 - b0 ? 0 : (a.q_pos ? a.q_pos[tok] : tok);
-          rrow[j] = (int32_t)clamp_row(a.rope, pos);
+          b0[k] = a.cu_q ? a.cu_q[bb] : bb * a.q_len;
+          b1[k] = a.cu_q ? a.cu_q[bb + 1] : (bb + 1) * a.q_len;
+        }
+      }
+      int64_t pos[NJ];
+#pragma unroll
+      for (int k = 0; k < NJ; ++k) {
+        const int j = j0 + k * (int)blockDim.x;
+        const int tt = j - (j / QTOK) * QTOK;
+        const int64_t tok = (int64_t)b0[k] + tt;
+        pos[k] = 0;
+        if (pro && j < a.batch * QTOK && tt < b1[k] - b0[k]) pos[k] = a.q_pos ? a.q_pos[tok] : tok;
+      }
+#pragma unroll
+      for (int k = 0; k < NJ; ++k) {
+        const int j = j0 + k * (int)blockDim.x;
+        if (stage_seq && j <= a.batch) seq_tab[j] = i32x2_t{p0[k], len[k]};
+        if constexpr (DQ) {
+          if (j < a.batch) {
+            int32_t rows = c1[k] - c0[k];
+            rows = rows < 0 ? 0 : (rows > a.q_len ? a.q_len : rows);
+            qmeta[j] = i32x2_t{c0[k], rows};
+          }
+          if (pro && j < D) w_tab[j] = wj[k];
+          if (pro && j < a.batch * QTOK) rrow[j] = (int32_t)clamp_row(a.rope, pos[k]);
         }
       }
     }
