@@ -588,6 +588,23 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
   }
   int last = ld.c.L - 1 - pos0;  // last valid row of the tile
   last = last > 0 ? last : 0;     // (never negative, even for a plan that disagrees with L)
+  // Generic paging: every load's page id read first, then the loads. An LDS read placed
+  // between two LDS-DMA instructions is awaited before the next one issues (the DMA
+  // writes LDS), which serialized a tile's 16 loads behind 16 LDS round trips.
+  uint32_t pid[KPW];
+  if (LAYOUT == PAGED) {
+#pragma unroll
+    for (int k = 0; k < KPW; ++k) {
+      const int i = wave + k * W;
+      if (i >= G::NI) break;
+      int row, coff, dst;
+      bool isk;
+      load_slot<D, F8>(i, lane, row, coff, isk, dst);
+      row = row < last ? row : last;
+      pid[k] = min((uint32_t)ids[row], a.page_last);
+    }
+  }
+  const bool unit_pages = a.page_size == 1;  // token paging: every position its own page
 #pragma unroll
   for (int k = 0; k < KPW; ++k) {
     const int i = wave + k * W;
@@ -610,9 +627,8 @@ __device__ __forceinline__ void issue_kv(const AttnArgs &a, const Loader &ld, ch
         if ((row >> 4) == q) page = pg[q];
       off = (uint64_t)page * (isk ? a.k_page_b : a.v_page_b) + ((uint32_t)p & a.page_mask) * tok_b;
     } else {
-      const uint32_t page = min((uint32_t)ids[row], a.page_last);
-      const uint32_t in_page = a.page_size == 1 ? 0u : (uint32_t)(p - (p / a.page_size) * a.page_size);
-      off = (uint64_t)page * (isk ? a.k_page_b : a.v_page_b) + in_page * tok_b;
+      const uint32_t in_page = unit_pages ? 0u : (uint32_t)(p - (p / a.page_size) * a.page_size);
+      off = (uint64_t)pid[k] * (isk ? a.k_page_b : a.v_page_b) + in_page * tok_b;
     }
     dma16(base + off + coff, stage + dst);
   }
