@@ -217,6 +217,9 @@ VIRTUAL_WORKLOADS = {
 TREE_WORKLOADS = {
     "tree-r8b-b1-n32": (1, 16, 16, 128, 32, 8192, 8192),
     "tree-r8b-b4-n8": (4, 16, 16, 128, 8, 1024, 8192),
+    # One candidate per request: the SGLang drafter's own cross-attention call at C3's shape
+    # (batch 64, 32/8 heads, contexts U[256, 8192]: C3's draw, pool slots permuted).
+    "c3shape-sglang-pool-b64": (64, 32, 8, 128, 1, 256, 8192),
 }
 
 
