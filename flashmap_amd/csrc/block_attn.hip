@@ -116,6 +116,7 @@ struct AttnArgs {
   int32_t nrb;                       // 16-row blocks (wavefronts) per unit
   int32_t num_shares;  // workgroups x replicas
   int32_t share_c;     // a unit's extra cost in tiles when the line is cut into shares (share_first_tiles)
+  int32_t *plan_out;   // set: the query pass's last workgroup writes the call's plan here
   float scale_log2;
   float v_scale;  // combine: scale of the context partials' values (1 but for verify calls)
   int32_t tail;   // verify calls: unit u's verify-token partial is slot units + num_shares + u
@@ -949,6 +950,39 @@ template <int D>
 __device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArgs &v, const u32x4_t (&qf)[D / 32], char *vs,
                               int64_t unit, int b, int h, int rg, int rb, int lane);
 
+// The step plan: both tile prefixes (32- and 64-position tiles) of the sequences' lengths
+// (CSR: indptr differences), plan[0 .. batch] and plan[batch + 1 ..], by the NT threads of
+// one workgroup (an inclusive scan per chunk of NT sequences). attn_plan_kernel runs it
+// alone; the query pass of a call without a plan runs it in one workgroup of its own.
+template <int NT>
+__device__ __forceinline__ void plan_prefixes(const int32_t *__restrict__ seqlens, int32_t batch,
+                                              int32_t *__restrict__ plan, int32_t csr) {
+  __shared__ int32_t buf[2][NT];
+  int32_t carry[2] = {0, 0};
+  int32_t *out[2] = {plan, plan + batch + 1};
+  if (threadIdx.x == 0) out[0][0] = 0, out[1][0] = 0;
+  for (int base = 0; base < batch; base += NT) {
+    const int i = base + threadIdx.x;
+    int32_t L = i < batch ? (csr ? seqlens[i + 1] - seqlens[i] : seqlens[i]) : 0;
+    L = L > 0 ? L : 0;
+    buf[0][threadIdx.x] = (L + TILE - 1) / TILE;
+    buf[1][threadIdx.x] = (L + TILE_F8 - 1) / TILE_F8;
+    __syncthreads();
+    for (int off = 1; off < NT; off <<= 1) {
+      const bool in = threadIdx.x >= (unsigned)off;
+      const int32_t add0 = in ? buf[0][threadIdx.x - off] : 0, add1 = in ? buf[1][threadIdx.x - off] : 0;
+      __syncthreads();
+      buf[0][threadIdx.x] += add0;
+      buf[1][threadIdx.x] += add1;
+      __syncthreads();
+    }
+    if (i < batch) out[0][i + 1] = carry[0] + buf[0][threadIdx.x], out[1][i + 1] = carry[1] + buf[1][threadIdx.x];
+    carry[0] += buf[0][NT - 1];
+    carry[1] += buf[1][NT - 1];
+    __syncthreads();
+  }
+}
+
 // The query rows of every unit in MFMA-block order: row r of unit (b, h, rg) is query
 // head h*G + R / q_len at draft token R % q_len, R = rg * 16 nrb + r, rows beyond the
 // group or the sequence's draft rows are zero. With the prologue requested, each row
@@ -958,6 +992,10 @@ __device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArg
 template <int D, bool VERIFY>
 __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, const VerifyArgs v) {
   constexpr int KT = D / 32;
+  if (a.plan_out != nullptr && blockIdx.x == gridDim.x - 1) {  // the call's plan (one launch fewer)
+    plan_prefixes<256>(a.seqlens, a.batch, a.plan_out, a.csr);
+    return;
+  }
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();  // (unit, row block)
   const int64_t units = (int64_t)a.batch * a.ups;
@@ -1005,6 +1043,10 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, con
 // One wavefront per 16-row block, lane (n, g) holding channels 32 t + 8 g .. + 7.
 template <int D>
 __global__ __launch_bounds__(256) void pack_queries_f8_kernel(const AttnArgs a) {
+  if (a.plan_out != nullptr && blockIdx.x == gridDim.x - 1) {  // the call's plan (one launch fewer)
+    plan_prefixes<256>(a.seqlens, a.batch, a.plan_out, a.csr);
+    return;
+  }
   constexpr int KT = D / 32;
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();  // (unit, row block)
@@ -2241,30 +2283,7 @@ __global__ __launch_bounds__(256) void attn_merge_wide_kernel(const AttnArgs a) 
 __global__ __launch_bounds__(1024) void attn_plan_kernel(const int32_t *__restrict__ seqlens,
                                                          int32_t batch, int32_t *__restrict__ plan,
                                                          int32_t csr) {
-  __shared__ int32_t buf[2][1024];
-  int32_t carry[2] = {0, 0};
-  int32_t *out[2] = {plan, plan + batch + 1};
-  if (threadIdx.x == 0) out[0][0] = 0, out[1][0] = 0;
-  for (int base = 0; base < batch; base += 1024) {
-    const int i = base + threadIdx.x;
-    int32_t L = i < batch ? (csr ? seqlens[i + 1] - seqlens[i] : seqlens[i]) : 0;
-    L = L > 0 ? L : 0;
-    buf[0][threadIdx.x] = (L + TILE - 1) / TILE;
-    buf[1][threadIdx.x] = (L + TILE_F8 - 1) / TILE_F8;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const bool in = threadIdx.x >= (unsigned)off;
-      const int32_t add0 = in ? buf[0][threadIdx.x - off] : 0, add1 = in ? buf[1][threadIdx.x - off] : 0;
-      __syncthreads();
-      buf[0][threadIdx.x] += add0;
-      buf[1][threadIdx.x] += add1;
-      __syncthreads();
-    }
-    if (i < batch) out[0][i + 1] = carry[0] + buf[0][threadIdx.x], out[1][i + 1] = carry[1] + buf[1][threadIdx.x];
-    carry[0] += buf[0][1023];
-    carry[1] += buf[1][1023];
-    __syncthreads();
-  }
+  plan_prefixes<1024>(seqlens, batch, plan, csr);
 }
 
 // ---------------------------------------------------------------------------------
@@ -2608,12 +2627,19 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   a.q_rs = (float *)(ws + sz.rs_off);
   a.part_lse = (float *)(ws + sz.lse_off);
   a.part_o = (uint16_t *)(ws + sz.o_off);
+  // A call without a plan makes its own: in the query pass's last workgroup when there is a
+  // query pass (one launch fewer), else with attn_plan_kernel.
+  const bool pass = qmode != Q_DIRECT;
   if (a.seqlens != nullptr) {
     const int32_t *plan = c.plan;
     if (need_plan) {
       int32_t *own = (int32_t *)(ws + sz.plan_off);
-      attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, own, a.csr);
-      FM_CHECK_HIP(hipGetLastError());
+      if (pass) {
+        a.plan_out = own;
+      } else {
+        attn_plan_kernel<<<1, 1024, 0, c.stream>>>(a.seqlens, c.batch, own, a.csr);
+        FM_CHECK_HIP(hipGetLastError());
+      }
       plan = own;
     }
     a.plan = plan + (a.f8 ? c.batch + 1 : 0);  // the prefix of this call's tile size
@@ -2621,7 +2647,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     a.plan = nullptr;
     a.uniform_tiles = (a.uniform_len + (a.f8 ? TILE_F8 : TILE) - 1) / (a.f8 ? TILE_F8 : TILE);
   }
-  const int64_t qblocks = (units * sz.rp.nrb + 3) / 4;
+  const int64_t qblocks = (units * sz.rp.nrb + 3) / 4 + (a.plan_out != nullptr ? 1 : 0);
   const VerifyArgs nov{};
   if (qmode == Q_DIRECT) {
     // no query pass: the attention kernel reads the rows and applies the prologue
