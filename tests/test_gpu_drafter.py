@@ -70,7 +70,6 @@ def test_draft_matches_reference(dev, name):
     assert same.float().mean() >= 0.99, f"greedy tokens equal on {same.float().mean():.3f} of the slots"
 
 
-
 def test_spec_generate_is_lossless(dev):
     from transformers import Qwen3Config, Qwen3ForCausalLM
 
