@@ -527,7 +527,8 @@ __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<
 // persistent kernel's two-replica workgroups (W consumers per replica). Measured, one
 // box, kernel: verify 211 -> 191 us, token-pool drafter at C3's shape 198 -> 185 us, at
 // batch 8 x 32768 positions 200 -> 189 us; one-replica workgroups (8 consumers, tree
-// drafting) got 13 % slower with it and keep the MFMA-ordered stage.
+// drafting) got 13 % slower with it, and vLLM's 16-position pages (whose sixteen rows lie
+// 512 bytes apart in one page) 2 % slower: both keep the MFMA-ordered stage.
 template <int LAYOUT, int D, bool F8, int W>
 __host__ __device__ constexpr bool krow() { return LAYOUT == PAGED && !F8 && D == 128 && replicas(W) == 2; }
 
