@@ -525,8 +525,8 @@ __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<
 // and head_dim 128, where the MFMA-ordered stage would have each load instruction gather
 // sixteen scattered pool rows (address translation then held the loads back), in the
 // persistent kernel's two-replica workgroups (W consumers per replica). Measured, one
-// box, kernel: verify 211 -> 191 us, token-pool drafter at C3's shape 198 -> 185 us, at
-// batch 8 x 32768 positions 200 -> 189 us; one-replica workgroups (8 consumers, tree
+// box, kernel: verify 211 -> 191 us, the drafter's call on a token pool at batch 64
+// (32/8 heads, 256-8192 positions) 198 -> 185 us, at batch 8 x 32768 positions 200 -> 189 us; one-replica workgroups (8 consumers, tree
 // drafting) got 13 % slower with it, and vLLM's 16-position pages (whose sixteen rows lie
 // 512 bytes apart in one page) 2 % slower: both keep the MFMA-ordered stage.
 template <int LAYOUT, int D, bool F8, int W>
@@ -2554,8 +2554,8 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     // Direct rows cost a prologue at every segment start, inside the workgroup's barrier
     // cycle (about 5000 shader cycles at 64 rows x D 128), which the cost cut of the line
     // absorbs (6 tiles per unit); the query pass costs a launch and one read + write of the
-    // rows. Measured: direct rows win up to one unit per share (C3's 512 units over 512
-    // shares: 176 us per call against 179 us with the pass); calls of more units than
+    // rows. Measured: direct rows win up to one unit per share (batch 64 x 8 KV heads, 512
+    // units over 512 shares: 176 us per call against 179 us with the pass); calls of more units than
     // shares keep the pass. FLASHMAP_QUERY_PASS=1 forces the pass, =0 the direct rows where
     // they apply; at one share cost both give the same bits.
     const int force = env_int("FLASHMAP_QUERY_PASS", -1);
@@ -2615,8 +2615,8 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // what a segment start and a partial hand-off cost the persistent kernel, measured best
   // at 2 tiles for bf16 (32 positions) and 4 for e4m3 (64 positions). Where the units span
   // more than four shares each on average, every share holds one or two segments whatever
-  // the cut, and an extra cost only unbalances shares of equal units (C4's 32768-position
-  // sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
+  // the cut, and an extra cost only unbalances shares of equal units (batch 8 of
+  // 32768-position sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
   // FLASHMAP_SHARE_COST overrides.
   const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares ? (a.f8 ? 4 : qmode == Q_DIRECT ? 6 : 2) : 0;
   a.share_c = small_tiles > 0 ? 0 : env_int("FLASHMAP_SHARE_COST", share_c);
