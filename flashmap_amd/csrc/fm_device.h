@@ -117,9 +117,8 @@ __device__ __forceinline__ u32x4_t load16(const void *p) {
 __device__ __forceinline__ void store16(void *p, u32x4_t v) { *reinterpret_cast<u32x4_t *>(p) = v; }
 // Non-temporal (streaming) store, for the bf16 query pass's packed rows and the merged
 // attention output: measured to shorten those two kernels (batch-64 paged drafter call:
-// 1.5-3 us per call). Not for
-// the split partials or the e4m3 packed rows, which their next reader then took longer to
-// fetch, nor for the cache writers, which it slowed.
+// 1.5-3 us per call). Not for the split partials or the e4m3 packed rows, which their next
+// reader then took longer to fetch, nor for the cache writers, which it slowed.
 __device__ __forceinline__ void store16_nt(void *p, u32x4_t v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(p));
 }
