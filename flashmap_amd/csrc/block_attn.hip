@@ -947,9 +947,20 @@ struct VerifyArgs {
   float scale_log2;            // softmax_scale * log2(e) of the tokens' scores
 };
 
+// The first TILE tokens' keys (K operands) and values (stage V layout) of a wavefront's
+// verify tokens, loaded before its query rows so that their latency overlaps the rows'.
+template <int D>
+struct VerifyChunk {
+  u32x4_t k[2][D / 32];
+  u32x4_t v[Geo<D>::NI - Geo<D>::KFRAGS];
+};
+
 template <int D>
 __device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArgs &v, const u32x4_t (&qf)[D / 32], char *vs,
-                              int64_t unit, int b, int h, int rg, int rb, int lane);
+                              int64_t unit, int b, int h, int rg, int rb, int lane, const VerifyChunk<D> &c0);
+template <int D>
+__device__ __forceinline__ void verify_chunk_load(const AttnArgs &a, const VerifyArgs &v, int b, int h, int j0,
+                                                  int lane, VerifyChunk<D> &c);
 
 // The step plan: both tile prefixes (32- and 64-position tiles) of the sequences' lengths
 // (CSR: indptr differences), plan[0 .. batch] and plan[batch + 1 ..], by the NT threads of
@@ -1010,6 +1021,8 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, con
   const int R = rg * 16 * a.nrb + r;
   const int gq = R / a.q_len, tq = R - gq * a.q_len;
   const bool valid = gq < a.group && tq < q_rows_of(a, b);
+  VerifyChunk<D> vc;
+  if constexpr (VERIFY) verify_chunk_load<D>(a, v, b, h, 0, lane, vc);
   const int64_t tok = q_token_index(a, b, valid ? tq : 0);
   const int64_t head = (int64_t)h * a.group + (valid ? gq : 0);
   const uint16_t *src = a.q + (a.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)(valid ? tq : 0) * a.q_st) +
@@ -1030,7 +1043,7 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, con
 #pragma unroll
     for (int t = 0; t < KT; ++t)
       if (!valid) qf[t] = u32x4_t{0, 0, 0, 0};
-    verify_tokens<D>(a, v, qf, vstage[wave_id()], unit, b, h, rg, rb, lane);
+    verify_tokens<D>(a, v, qf, vstage[wave_id()], unit, b, h, rg, rb, lane, vc);
   }
 }
 
@@ -1175,8 +1188,36 @@ __device__ __forceinline__ void store_partial_rows(const AttnArgs &a, const u32x
 // q_len read the last token (finite) and get P = 0. No branch surrounds the MFMA or the
 // transposing LDS reads, which need every lane.
 template <int D>
+__device__ __forceinline__ void verify_chunk_load(const AttnArgs &a, const VerifyArgs &v, int b, int h, int j0,
+                                                  int lane, VerifyChunk<D> &c) {
+  using G = Geo<D>;
+  constexpr int KT = D / 32;
+  const int n = lane & 15, g = lane >> 4;
+  const int L = a.q_len;
+  const int64_t tok0 = (int64_t)b * L;
+  const int last = L - 1 - j0;  // last token of the chunk
+  const uint16_t *kb = v.k + (int64_t)h * v.k_sh;
+  const uint16_t *vb = v.v + (int64_t)h * v.v_sh;
+#pragma unroll
+  for (int i = G::KFRAGS; i < G::NI; ++i) {
+    int row, coff, dst;
+    bool isk;
+    load_slot<D>(i, lane, row, coff, isk, dst);
+    const int j = j0 + (row < last ? row : last);
+    c.v[i - G::KFRAGS] = load16(reinterpret_cast<const char *>(vb + (tok0 + j) * v.v_st) + coff);
+  }
+#pragma unroll
+  for (int pb = 0; pb < 2; ++pb) {
+    const int jr = 16 * pb + n;
+    const uint16_t *kr = kb + (tok0 + j0 + (jr < last ? jr : last)) * v.k_st + 8 * g;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) c.k[pb][t] = load16(kr + 32 * t);
+  }
+}
+
+template <int D>
 __device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArgs &v, const u32x4_t (&qf)[D / 32], char *vs,
-                              int64_t unit, int b, int h, int rg, int rb, int lane) {
+                              int64_t unit, int b, int h, int rg, int rb, int lane, const VerifyChunk<D> &c0) {
   using G = Geo<D>;
   constexpr int KT = D / 32;
   const int n = lane & 15, g = lane >> 4;
@@ -1192,32 +1233,27 @@ __device__ __forceinline__ void verify_tokens(const AttnArgs &a, const VerifyArg
   } else if (v.mode == 2) {
     mrow = (tok0 + tq) * L;
   }
-  const uint16_t *kb = v.k + (int64_t)h * v.k_sh;
-  const uint16_t *vb = v.v + (int64_t)h * v.v_sh;
   f32x4_t acc[G::DB];
 #pragma unroll
   for (int db = 0; db < G::DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
+  VerifyChunk<D> c = c0;  // the first chunk's loads were issued ahead
   for (int j0 = 0; j0 < L; j0 += TILE) {
-    const int last = L - 1 - j0;  // last token of the chunk
+    if (j0 > 0) verify_chunk_load<D>(a, v, b, h, j0, lane, c);
 #pragma unroll
     for (int i = G::KFRAGS; i < G::NI; ++i) {  // values, as the stage's V blocks
       int row, coff, dst;
       bool isk;
       load_slot<D>(i, lane, row, coff, isk, dst);
-      const int j = j0 + (row < last ? row : last);
-      *reinterpret_cast<u32x4_t *>(vs + (dst - G::KBYTES) + lane * 16) =
-          load16(reinterpret_cast<const char *>(vb + (tok0 + j) * v.v_st) + coff);
+      *reinterpret_cast<u32x4_t *>(vs + (dst - G::KBYTES) + lane * 16) = c.v[i - G::KFRAGS];
     }
     f32x4_t s[2];
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb) {  // S^T[token 16 pb + 4 g + i][row n]
-      const int jr = 16 * pb + n;
-      const uint16_t *kr = kb + (tok0 + j0 + (jr < last ? jr : last)) * v.k_st + 8 * g;
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < KT; ++t) c = mfma_16x16x32(load16(kr + 32 * t), qf[t], c);
-      s[pb] = c;
+      for (int t = 0; t < KT; ++t) sc = mfma_16x16x32(c.k[pb][t], qf[t], sc);
+      s[pb] = sc;
     }
     float mx = -INFINITY;
 #pragma unroll
