@@ -530,7 +530,7 @@ __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<
 // drafting) got 13 % slower with it, and vLLM's 16-position pages (whose sixteen rows lie
 // 512 bytes apart in one page) 2 % slower: both keep the MFMA-ordered stage.
 template <int LAYOUT, int D, bool F8, int W>
-__host__ __device__ constexpr bool krow() { return LAYOUT == PAGED && !F8 && D == 128 && replicas(W) == 2; }
+__host__ __device__ constexpr bool krow() { return LAYOUT == PAGED && D == 128 && replicas(W) == 2; }
 
 // Row (within the tile) and byte offset within the row of this lane's k-th load of a
 // tile, and whether it is a K load. Load i = wave + k*W of the NI loads (K blocks, then
@@ -547,10 +547,18 @@ __device__ __forceinline__ void load_slot(int i, int lane, int &row, int &coff, 
       // of the stage's K (256 bytes each) holds tile row (i & 3) + 16 (i >> 2) + 4 g (the
       // rows this lane also loads for V, so one pool address per row), its 16-byte chunk p
       // being the row's chunk p ^ (s & 15). compute_tile reads the fragments from there.
-      static_assert(!F8 && D == 128, "row-major K stages are bf16 at head_dim 128");
-      const int slot = 4 * i + g;
-      row = (i & 3) + 16 * (i >> 2) + 4 * g;
-      coff = 16 * (n ^ (slot & 15));
+      static_assert(D == 128, "row-major K stages are head_dim 128");
+      if constexpr (F8) {
+        // e4m3 rows of 128 bytes: instruction i loads rows 8 i .. 8 i + 7 (eight lanes a
+        // row; the rows this lane also loads for V), slot chunk p holding the row's chunk
+        // p ^ ((row >> 1) & 7).
+        row = 8 * i + (lane >> 3);
+        coff = 16 * ((lane & 7) ^ ((row >> 1) & 7));
+      } else {
+        const int slot = 4 * i + g;
+        row = (i & 3) + 16 * (i >> 2) + 4 * g;
+        coff = 16 * (n ^ (slot & 15));
+      }
     } else {
       const int pb = i / G::KC, c = i - (i / G::KC) * G::KC;
       row = 16 * pb + n;
@@ -844,10 +852,27 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
     constexpr int NK = NH * G::KC;
     static_assert(NK == 8 || NK == 4, "head_dim 128 or 64");
     typedef __attribute__((address_space(3))) const char lds_char_t;
-    const uint32_t ka = (uint32_t)(uintptr_t)(lds_char_t *)(stage + lane * 16);
     u32x4_t kf[NK];
+    if constexpr (KROW) {
+      // K by rows (load_slot): fragment (pb, c) of lane (n, g) is row 16 pb + n, bytes
+      // 64 c + 16 g, at 128 (16 pb + n) + 64 (c ^ (m >> 2)) + 16 (g ^ (m & 3)) with
+      // m = (n >> 1) & 7: eight (and sixteen) lanes read distinct 16-byte bank groups.
+      static_assert(NK == 8, "row-major K stages are head_dim 128");
+      const int n = lane & 15, m = (n >> 1) & 7;
+      const uint32_t k0 = (uint32_t)(uintptr_t)(lds_char_t *)(stage + 128 * n + 16 * (g ^ (m & 3)));
 #pragma unroll
-    for (int i = 0; i < NK; ++i) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[i]) : "v"(ka), "i"(1024 * i));
+      for (int c = 0; c < 2; ++c) {
+        const uint32_t kc = k0 + 64 * (c ^ (m >> 2));
+        asm volatile("ds_read_b128 %0, %1" : "=v"(kf[c]) : "v"(kc));
+        asm volatile("ds_read_b128 %0, %1 offset:2048" : "=v"(kf[2 + c]) : "v"(kc));
+        asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(kf[4 + c]) : "v"(kc));
+        asm volatile("ds_read_b128 %0, %1 offset:6144" : "=v"(kf[6 + c]) : "v"(kc));
+      }
+    } else {
+      const uint32_t ka = (uint32_t)(uintptr_t)(lds_char_t *)(stage + lane * 16);
+#pragma unroll
+      for (int i = 0; i < NK; ++i) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(kf[i]) : "v"(ka), "i"(1024 * i));
+    }
     if constexpr (NK == 8) {
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]),
