@@ -221,6 +221,11 @@ TREE_WORKLOADS = {
     # (batch 64, 32/8 heads, contexts U[256, 8192]: C3's draw, pool slots permuted).
     "c3shape-sglang-pool-b64": (64, 32, 8, 128, 1, 256, 8192),
 }
+# The same calls onto e4m3 pools (flashmap_sglang::paged_cross_attention_fp8): name -> the
+# bf16 workload whose shape and draw it takes (the pools' values rounded to e4m3).
+TREE_FP8_WORKLOADS = {
+    "c3shape-sglang-pool-b64-fp8": "c3shape-sglang-pool-b64",
+}
 
 
 # The draft step's token selection over bf16 logits: name -> (rows, vocabulary, mode).
@@ -669,7 +674,8 @@ def run_tree(args, dev) -> dict:
     side by side: query packing, the split-KV stream and the combine."""
     from flashmap_amd import ops
 
-    requests, hq, hkv, d, n_cand, lo, hi = TREE_WORKLOADS[args.workload]
+    fp8 = args.workload in TREE_FP8_WORKLOADS
+    requests, hq, hkv, d, n_cand, lo, hi = TREE_WORKLOADS[TREE_FP8_WORKLOADS.get(args.workload, args.workload)]
     k_rows = 16
     q_len = n_cand * k_rows
     g = torch.Generator().manual_seed(0)
@@ -682,17 +688,23 @@ def run_tree(args, dev) -> dict:
         pt[b, :int(lens[b])] = slots[o:o + int(lens[b])]
         o += int(lens[b])
     q = torch.randn(requests, q_len, hq, d, generator=g).bfloat16().to(dev)
-    kb = torch.randn(ctx, hkv, d, generator=g).bfloat16().to(dev)
-    vb = torch.randn(ctx, hkv, d, generator=g).bfloat16().to(dev)
+    kb = torch.randn(ctx, hkv, d, generator=g).bfloat16()
+    vb = torch.randn(ctx, hkv, d, generator=g).bfloat16()
+    if fp8:  # e4m3 pools (round to nearest even, saturating at 448)
+        kb, vb = (x.float().clamp(-448.0, 448.0).to(torch.float8_e4m3fn) for x in (kb, vb))
+    kb, vb = kb.to(dev), vb.to(dev)
     lens_d, pt_d = lens.to(dev, torch.int32), pt.to(dev)
     plan = ops.attention_plan(lens_d)
     out = torch.empty_like(q)
 
     def call():
-        ops.block_attention_token_paged(q, kb, vb, lens_d, pt_d, plan=plan, out=out)
+        if fp8:
+            ops.block_attention_token_paged_fp8(q, kb, vb, lens_d, pt_d, plan=plan, out=out)
+        else:
+            ops.block_attention_token_paged(q, kb, vb, lens_d, pt_d, plan=plan, out=out)
 
     ms, kernel_ms, timing = _time_call(call, args)
-    kv = ctx * hkv * d * 2 * 2
+    kv = ctx * hkv * d * 2 * (1 if fp8 else 2)
     total = kv + 4 * ctx + 4 * requests + 2 * requests * q_len * hq * d * 2
     flops = 4 * q_len * hq * d * ctx
     gbs = total / (kernel_ms * 1e-3) / 1e9
@@ -703,10 +715,12 @@ def run_tree(args, dev) -> dict:
         "metric": "tree-drafting cross-attn µs/call, n_cand x 16 rows per request, 1 GPU",
         "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic: seeded CPU draw (lengths, pool slots, q, K/V)",
+        "dtype": "e4m3 K/V, bf16 q" if fp8 else "bf16",
+        "data": "synthetic: seeded CPU draw (lengths, pool slots, q, K/V)",
         "config": {"workload": args.workload, "requests": requests, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
                    "candidates": n_cand, "q_rows_per_request": q_len, "ctx_lo": lo, "ctx_hi": hi, "ctx_sum": ctx,
-                   "layout": "sglang token pool (pool, kv_heads, head_dim), page table"},
+                   "layout": "sglang token pool (pool, kv_heads, head_dim), page table",
+                   "kv_dtype": "e4m3" if fp8 else "bf16"},
         "roofline": ({"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": round(mfma_frac, 4)} if mfma_bound else
                      {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -717,22 +731,27 @@ def run_tree(args, dev) -> dict:
                                "flops_per_launch": flops, "kernel_us": round(kernel_ms * 1e3, 2)})
     result.update(_timing_fields(timing))
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = tree_cpu_baseline(q, kb, vb, lens, pt, args.cpu_budget)
+        result["cpu_baseline"] = tree_cpu_baseline(q, kb, vb, lens, pt, args.cpu_budget, fp8)
     return result
 
 
-def tree_cpu_baseline(q, kb, vb, lens, pt, budget_s) -> dict:
-    """The token-paged oracle on the host cores, request by request until the budget is
-    spent, scaled to the whole call by context positions."""
+def tree_cpu_baseline(q, kb, vb, lens, pt, budget_s, fp8: bool = False) -> dict:
+    """The token-paged oracle (the e4m3 one for e4m3 pools) on the host cores, request by
+    request until the budget is spent, scaled to the whole call by context positions."""
     from oracle import attention as ref
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     kc, vc, qc = kb.cpu(), vb.cpu(), q.cpu()
+    if fp8:  # widened once (exact): the oracle would widen the whole pool for every request
+        kc, vc = kc.float(), vc.float()
     done_l = done = 0
     t0 = time.perf_counter()
     for b in range(len(lens)):
-        ref.block_attention_token_paged(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
+        if fp8:
+            ref.block_attention_token_paged_fp8(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
+        else:
+            ref.block_attention_token_paged(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
         done_l += int(lens[b])
         done += 1
         if time.perf_counter() - t0 > budget_s:
@@ -740,7 +759,8 @@ def tree_cpu_baseline(q, kb, vb, lens, pt, budget_s) -> dict:
     elapsed = time.perf_counter() - t0
     return {"value": round(elapsed * int(lens.sum()) / done_l * 1e6, 1), "unit": "us/call", "cores": cores,
             "kind": "port", "sample": f"first {done} of {len(lens)} requests ({done_l} context positions): "
-                                      "fp32 oracle token-paged attention, scaled by positions"}
+                                      f"fp32 oracle token-paged{' e4m3 (pools widened to fp32 once)' if fp8 else ''} "
+                                      "attention, scaled by positions"}
 
 
 def run_verify(args, dev) -> dict:
@@ -845,7 +865,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64",
                     choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS)
-                    + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS) + sorted(SELECT_WORKLOADS)
+                    + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS) + sorted(TREE_FP8_WORKLOADS)
+                    + sorted(SELECT_WORKLOADS)
                     + sorted(CONTIG_WORKLOADS) + sorted(DRAFT_STEP_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -874,7 +895,7 @@ def main() -> int:
     if args.workload in VERIFY_WORKLOADS:
         print(json.dumps(run_verify(args, dev)))
         return 0
-    if args.workload in TREE_WORKLOADS:
+    if args.workload in TREE_WORKLOADS or args.workload in TREE_FP8_WORKLOADS:
         print(json.dumps(run_tree(args, dev)))
         return 0
     if args.workload in SELECT_WORKLOADS:
