@@ -503,3 +503,29 @@ def test_share_cost_cuts(dev, monkeypatch, cost, qpass):
     got = o.block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
                                   t, lmax, d ** -0.5, prologue=pro)
     check_close(got, want)
+
+
+@pytest.mark.parametrize("qpass", ["1", "0"])
+def test_own_plan_equals_step_plan(dev, monkeypatch, qpass):
+    """A call given no step plan computes its own (in one extra workgroup of its query pass
+    when it has one, else with a launch of its own): the same bits as the call given the
+    step plan of ops.attention_plan."""
+    g = gen(49)
+    hq, hkv, d, t, page = 32, 8, 128, 16, 16
+    lens = torch.tensor([0, 5, 700, 1, 2000, 31, 129, 450])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total).to(dev)
+    cu = (torch.arange(b + 1, dtype=torch.int32) * t).to(dev)
+    lens_d = lens.to(dev, torch.int32)
+    monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")
+    monkeypatch.setenv("FLASHMAP_QUERY_PASS", qpass)
+    o = ops()
+    own = o.block_attention_paged(q.to(dev), cache, cu, lens_d, bt.to(dev), t, lmax, d ** -0.5)
+    step = o.block_attention_paged(q.to(dev), cache, cu, lens_d, bt.to(dev), t, lmax, d ** -0.5,
+                                   plan=o.attention_plan(lens_d))
+    assert torch.equal(own, step)

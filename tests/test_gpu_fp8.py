@@ -208,3 +208,22 @@ def test_paged_fp8_share_cost_cuts(dev, monkeypatch, cost):
                                           k_rows, 3000, d ** -0.5, descales=desc.to(dev))
     torch.cuda.synchronize()
     check_close(got.cpu().float(), ref.block_attention_paged_vllm_fp8(q8, cache, cu, lens, bt, d ** -0.5, desc))
+
+
+def test_paged_fp8_own_plan_equals_step_plan(dev):
+    """An e4m3 call given no step plan computes its own in its query pass: the same bits as
+    the call given ops.attention_plan's (whose second prefix counts 64-position tiles)."""
+    g = gen(98)
+    hq, hkv, d, page, k_rows = 32, 8, 128, 16, 16
+    lens = torch.tensor([0, 5, 65, 700, 1, 3000, 63, 450])
+    bs = len(lens)
+    bt, total = paged_layout(lens.tolist(), page, g)
+    cache = _e4m3((total, hkv, page, 2 * d), g).to(dev)
+    q8 = _e4m3((bs * k_rows, hq, d), g).to(dev)
+    cu = torch.arange(0, bs * k_rows + 1, k_rows, dtype=torch.int32).to(dev)
+    lens_d = lens.to(dev, torch.int32)
+    o = ops()
+    own = o.block_attention_paged_fp8(q8, cache, cu, lens_d, bt.to(dev), k_rows, 3000, d ** -0.5)
+    step = o.block_attention_paged_fp8(q8, cache, cu, lens_d, bt.to(dev), k_rows, 3000, d ** -0.5,
+                                       plan=o.attention_plan(lens_d))
+    assert torch.equal(own, step)
