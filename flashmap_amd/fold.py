@@ -1,20 +1,25 @@
-"""Load-time folds of the one-jump draft step, with the API of the reference's
-flashmap/vllm/fold.py (pure torch: computed once when the drafter is prepared, off the
-per-step path).
+"""Weight folds the vLLM plugin's draft step applies once, when the drafter is prepared
+(the public names and signatures of the reference's flashmap/vllm/fold.py, which the
+plugin's ``prepare`` imports; pure torch, nothing here runs per step).
 
-- ``fold_noise``: a one-jump draft reads its starting noise ``x0 ~ N(0, I_V)`` only as
-  ``x_embed(noise_norm(x0 @ E))``. ``x0 @ E`` is Gaussian with covariance ``E^T E = Q
-  Lambda Q^T``, so it is drawn as ``z @ A``, ``z ~ N(0, I_H)``, ``A = sqrt(Lambda) Q^T``;
-  then ``A A^T = Lambda`` makes the norm's mean square ``(z^2 @ lambda) / H``, and the
-  norm weight ``w`` and ``x_embed``'s weight fold into one matrix:
-  ``x_embed(noise_norm(z @ A)) = rsqrt(z^2 @ lambda / H + eps) * (z @ M^T) + b`` with
-  ``M = W_x diag(w) A^T`` (flashmap/vllm/fold.py:1-15, 45-75).
-- ``fold_head``: the DiT's output head (``D -> H`` with bias) followed by the target's
-  LM head (``H -> V``, no nonlinearity between) as one ``(V, D)`` weight and bias
-  (flashmap/vllm/fold.py:78-100).
+Noise. A draft of one jump starts from Gaussian noise over the vocabulary and reads it
+through one path only: the embedding ``E (V, H)``, then the noise norm, then ``x_embed``.
+The embedded noise is Gaussian with covariance ``E^T E``. Writing that covariance's
+eigendecomposition as ``Q diag(lambda) Q^T`` and ``A = diag(sqrt(lambda)) Q^T``, the same
+distribution comes from ``z @ A`` with ``z`` standard normal of width ``H`` instead of
+``V``. Because the rows of ``A`` are orthogonal (``A A^T = diag(lambda)``), the norm's mean
+square of ``z @ A`` is ``sum_i lambda_i z_i^2 / H``, so only a per-row scale is left to
+compute at run time, and the noise norm's weights ``w`` and ``x_embed``'s weight ``W_x``
+multiply with ``A`` into one ``(D, H)`` matrix ``M = W_x diag(w) A^T``
+(flashmap/vllm/fold.py:45-75): ``x_embed(noise_norm(z @ A)) = (z @ M^T) / rms + b``.
 
-The per-step use of the folded noise is ``ops.noise_rows`` + one GEMM +
-``ops.adaln_residual`` with a per-row gate (see ``flashmap_amd.draft_step``); the folded
+Head. The DiT's output projection ``(D -> H, with bias)`` feeds the target's LM head
+``(H -> V)`` directly; as both are linear, their product ``lm_head @ W_head`` and the
+projected bias ``lm_head @ b_head`` replace the pair with one ``(V, D)`` GEMM
+(flashmap/vllm/fold.py:78-100).
+
+At run time the folded noise is ``ops.noise_rows`` (the row scales) + one GEMM +
+``ops.adaln_residual`` with a per-row gate (``flashmap_amd.draft_step``), and the folded
 head is one GEMM followed by ``split_argmax`` (the gfx950 argmax kernel).
 """
 
@@ -74,9 +79,10 @@ def fold_noise(embedding: torch.Tensor, noise_norm_weight: torch.Tensor, x_embed
 @torch.no_grad()
 def fold_head(lm_head: torch.Tensor, head_weight: torch.Tensor, head_bias: torch.Tensor,
               rows: torch.Tensor | None = None, chunk: int = 8192) -> tuple[torch.Tensor, torch.Tensor]:
-    """``(lm_head[rows] @ W_head, lm_head[rows] @ b_head)``: one ``(len(rows), D)`` weight
-    and bias in the LM head's dtype, products in float32, ``chunk`` vocabulary rows at a
-    time (all rows when ``rows`` is None)."""
+    """The DiT head and the LM head as one linear map over the vocabulary rows ``rows``
+    (every row when None): weight ``lm_head[rows] @ W_head`` ``(len(rows), D)`` and bias
+    ``lm_head[rows] @ b_head``, multiplied in float32 and stored in the LM head's dtype,
+    ``chunk`` rows at a time so the float32 copies stay small."""
     count = lm_head.shape[0] if rows is None else rows.numel()
     weight = torch.empty(count, head_weight.shape[1], dtype=lm_head.dtype, device=lm_head.device)
     bias = torch.empty(count, dtype=lm_head.dtype, device=lm_head.device)

@@ -387,6 +387,13 @@ def block_attention_paged(
     return prep.out
 
 
+def static_scratch_init() -> None:
+    """Sets up :func:`block_attention_paged_static` on the current device (the scratch
+    array's address and the host-side caches its first call would fill); call it before
+    capturing that first call into a graph."""
+    call("fm_static_scratch_init")
+
+
 def block_attention_paged_static(
     query: torch.Tensor,
     kv_cache: torch.Tensor,
@@ -1213,6 +1220,11 @@ def noise_rows(z: torch.Tensor, eigvals: torch.Tensor, eps: float, gain: float,
     _need_numel(lam, hidden, "eigvals")
     if z_bf16 is None:
         z_bf16 = torch.empty(rows, hidden, dtype=torch.bfloat16, device=z.device)
+    elif (z_bf16.dtype != torch.bfloat16 or tuple(z_bf16.shape) != (rows, hidden) or z_bf16.stride(-1) != 1
+          or z_bf16.stride(0) % 4 or z_bf16.data_ptr() % 8):
+        raise ValueError(f"z_bf16 must be bf16 ({rows}, {hidden}) with unit channel stride, a row stride "
+                         f"of a multiple of 4 and 8-byte alignment; got {z_bf16.dtype} {tuple(z_bf16.shape)} "
+                         f"strides {z_bf16.stride()}")
     scale = torch.empty(rows, dtype=torch.bfloat16, device=z.device)
     if rows:
         call("fm_noise_rows", z.data_ptr(), rows, hidden, z.stride(0), lam.data_ptr(), float(eps), float(gain),

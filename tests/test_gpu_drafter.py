@@ -6,8 +6,8 @@
   one bf16 ulp of the largest logits is 0.4-0.8 %) and 0.1 % of the mean logit (mean),
   the -inf pattern of a state vocabulary exact, and the greedy draft tokens equal on
   every slot whose reference top-2 margin exceeds twice the observed error -- at least
-  85 % of the slots (the others are within bf16 rounding of a tie) -- and on at least 99 %
-  of all slots (measured: all of them).
+  85 % of the slots -- and, with these fixed weights and noise, on every slot (the
+  greedy-token identity the drop-in must keep).
 - ``spec_generate`` at temperature 0 is lossless: it returns the target's own greedy
   decoding (the property flashmap/modeling_flashmap.py:525-528 states), on a tiny
   random-init Qwen3 target.
@@ -65,9 +65,7 @@ def test_draft_matches_reference(dev, name):
           f"equal on {same.float().mean():.3f} of all slots", flush=True)
     assert clear.float().mean() >= 0.85
     assert same[clear].all()
-    # Measured: equal on every slot (1.000) for both cases; a near-tie flipped by bf16 rounding
-    # is the only allowed difference.
-    assert same.float().mean() >= 0.99, f"greedy tokens equal on {same.float().mean():.3f} of the slots"
+    assert same.all(), f"greedy draft tokens equal on {same.float().mean():.3f} of the slots, not all"
 
 
 def test_spec_generate_is_lossless(dev):
