@@ -49,6 +49,7 @@ SIGNATURES: dict[str, tuple] = {
          *_PROLOGUE, *_SPLIT],
     ),
     "fm_static_scratch_bytes": (c_size_t, []),
+    "fm_static_scratch_init": (c_int, []),
     "fm_block_attn_paged_static": (
         c_int,
         [*_Q, P, I64, I64, I64, I64, I64, I32, P, I64, I64, P, I32, I32, I32, I32, I32, I32, F32,
@@ -106,6 +107,7 @@ SIGNATURES: dict[str, tuple] = {
     "fm_profile_enable": (c_int, [c_int]),
     "fm_clock_probe": (c_int, [P, ctypes.c_uint64, P]),
     "fm_profile_read": (c_int, [ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]),
+    "fm_tuning_reload": (c_int, []),
 }
 
 _lib = None

@@ -50,6 +50,8 @@
 #include <math.h>
 #include <stddef.h>
 
+#include <atomic>
+#include <climits>
 #include <mutex>
 #include <type_traits>
 
@@ -2141,8 +2143,8 @@ struct RowMerge {
 // the loads are gathered into registers explicitly), each batch merged relative to its
 // own largest LSE and then into the running merge. MB = 8 takes about three times the
 // registers of MB = 2 (121 against 42 VGPRs at D 128), which halves the combine's
-// occupancy: full batches (about two segments per unit) use 2, calls of few units
-// split over many shares 8.
+// occupancy: the host picks the smallest MB of 2, 4 and 8 that holds a unit's average
+// segment count.
 template <int D, int MB>
 __device__ __forceinline__ void merge_partials(const AttnArgs &a, int64_t unit, int b, int ul, int r, int c,
                                                float vs, RowMerge &mg) {
@@ -2446,10 +2448,37 @@ static RowPlan row_plan(int group, int q_len) {
   return p;
 }
 
-static int env_int(const char *name, int dflt) {
+// Tuning overrides from the environment (FLASHMAP_*), read once, at the first call, and
+// again only on fm_tuning_reload(): the launch path reads no environment. INT_MIN: unset.
+struct Tuning {
+  std::atomic<int> min_tiles{INT_MIN}, workgroups{INT_MIN}, small_tiles{INT_MIN}, query_pass{INT_MIN},
+      share_cost{INT_MIN}, combine_mb{INT_MIN};
+};
+static Tuning g_tuning;
+static std::once_flag g_tuning_once;
+
+static int env_value(const char *name) {
   const char *v = getenv(name);
-  if (v == nullptr || *v == 0) return dflt;
-  return atoi(v);
+  return (v == nullptr || *v == 0) ? INT_MIN : atoi(v);
+}
+
+static void read_tuning() {
+  g_tuning.min_tiles = env_value("FLASHMAP_SPLITKV_MIN_TILES");
+  g_tuning.workgroups = env_value("FLASHMAP_SPLITKV_WORKGROUPS");
+  g_tuning.small_tiles = env_value("FLASHMAP_SMALL_TILES");
+  g_tuning.query_pass = env_value("FLASHMAP_QUERY_PASS");
+  g_tuning.share_cost = env_value("FLASHMAP_SHARE_COST");
+  g_tuning.combine_mb = env_value("FLASHMAP_COMBINE_MB");
+}
+
+static const Tuning &tuning() {
+  std::call_once(g_tuning_once, read_tuning);
+  return g_tuning;
+}
+
+static int tuned(const std::atomic<int> &v, int dflt) {
+  const int x = v.load(std::memory_order_relaxed);
+  return x == INT_MIN ? dflt : x;
 }
 
 // Workgroups resident per CU for a kernel (cached).
@@ -2489,10 +2518,11 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
   const int tile = qmode == Q_F8 ? TILE_F8 : TILE;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + tile - 1) / tile);
-  const int min_tiles = env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) > 0 ? env_int("FLASHMAP_SPLITKV_MIN_TILES", 8) : 1;
+  const Tuning &tu = tuning();
+  const int min_tiles = tuned(tu.min_tiles, 8) > 0 ? tuned(tu.min_tiles, 8) : 1;
   const int r = replicas(sz->rp.nrb);
   int64_t nw = (int64_t)info.cus * occupancy(k, 64 * (sz->rp.nrb + 1) * r);
-  const int cap = env_int("FLASHMAP_SPLITKV_WORKGROUPS", 0);
+  const int cap = tuned(tu.workgroups, 0);
   if (cap > 0) nw = cap;
   const int64_t want = (tiles_bound + min_tiles - 1) / min_tiles;  // shares worth splitting
   if ((want + r - 1) / r < nw) nw = (want + r - 1) / r;
@@ -2534,7 +2564,7 @@ static int small_tiles_for(int layout, int batch, int q_len, int hq, int hkv, in
   const int64_t tiles_bound = (int64_t)hkv * rp.rgroups * batch * (((int64_t)max_k + TILE - 1) / TILE);
   if (tiles_bound > (int64_t)info.cus * SMALL_TILES || select_small(layout, d, rp.nrb) == nullptr) return 0;
   int tps = (int)((tiles_bound + info.cus - 1) / info.cus);
-  tps = env_int("FLASHMAP_SMALL_TILES", tps);
+  tps = tuned(tuning().small_tiles, tps);
   tps = tps > SMALL_TILES ? SMALL_TILES : tps;
   return tps > 0 ? tps : 0;
 }
@@ -2619,7 +2649,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     // units over 512 shares: 176 us per call against 179 us with the pass); calls of more units than
     // shares keep the pass. FLASHMAP_QUERY_PASS=1 forces the pass, =0 the direct rows where
     // they apply; at one share cost both give the same bits.
-    const int force = env_int("FLASHMAP_QUERY_PASS", -1);
+    const int force = tuned(tuning().query_pass, -1);
     const int64_t units = (int64_t)c.batch * c.hkv * rp.rgroups;
     const bool small = units <= sz.num_shares;
     if (fast_rope && c.batch <= cap && (force == 0 || (force < 0 && small))) qmode = Q_DIRECT;
@@ -2680,7 +2710,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // 32768-position sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
   // FLASHMAP_SHARE_COST overrides.
   const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares ? (a.f8 ? 4 : qmode == Q_DIRECT ? 6 : 2) : 0;
-  a.share_c = small_tiles > 0 ? 0 : env_int("FLASHMAP_SHARE_COST", share_c);
+  a.share_c = small_tiles > 0 ? 0 : tuned(tuning().share_cost, share_c);
   if (a.share_c < 0) a.share_c = 0;
   a.tail = vf != nullptr;
   if (!a.tail) a.v_scale = 1.f;
@@ -2747,20 +2777,24 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     FM_CHECK_HIP(hipGetLastError());
     return FM_OK;
   }
-  // One workgroup of 2 D threads per 16-row block; units split into many segments (a
-  // call of few units over the whole grid) merge their partials 8 at a time.
+  // One workgroup of 2 D threads per 16-row block, merging a unit's partials MB at a time:
+  // MB about the segments a unit has (a segment per share it touches: shares / units + 1
+  // on average), so that most units take one memory round trip at the fewest registers.
   const int64_t cblocks = units * sz.rp.nrb;
   FM_REQUIRE(cblocks < (1ll << 31), "too many units");
-  const bool many = units * 2 <= sz.num_shares;
+  const int64_t segs = (sz.num_shares + units - 1) / units + 1;
+  int mb = tuned(tuning().combine_mb, segs <= 2 ? 2 : segs <= 4 ? 4 : 8);
+  mb = mb <= 2 ? 2 : mb <= 4 ? 4 : 8;
   const dim3 cg((unsigned)cblocks);
-  if (c.d == 128 && many)
-    attn_combine_kernel<128, 8><<<cg, dim3(256), 0, c.stream>>>(a);
-  else if (c.d == 128)
-    attn_combine_kernel<128, 2><<<cg, dim3(256), 0, c.stream>>>(a);
-  else if (many)
-    attn_combine_kernel<64, 8><<<cg, dim3(128), 0, c.stream>>>(a);
-  else
-    attn_combine_kernel<64, 2><<<cg, dim3(128), 0, c.stream>>>(a);
+  if (c.d == 128) {
+    if (mb == 2) attn_combine_kernel<128, 2><<<cg, dim3(256), 0, c.stream>>>(a);
+    else if (mb == 4) attn_combine_kernel<128, 4><<<cg, dim3(256), 0, c.stream>>>(a);
+    else attn_combine_kernel<128, 8><<<cg, dim3(256), 0, c.stream>>>(a);
+  } else {
+    if (mb == 2) attn_combine_kernel<64, 2><<<cg, dim3(128), 0, c.stream>>>(a);
+    else if (mb == 4) attn_combine_kernel<64, 4><<<cg, dim3(128), 0, c.stream>>>(a);
+    else attn_combine_kernel<64, 8><<<cg, dim3(128), 0, c.stream>>>(a);
+  }
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }
@@ -2938,6 +2972,32 @@ static int static_scratch(void **ptr) {
 }
 
 extern "C" size_t fm_static_scratch_bytes(void) { return STATIC_SCRATCH_BYTES; }
+
+// Set-up of fm_block_attn_paged_static on the current device, outside any graph capture:
+// the scratch array's address, the device's properties, the tuning overrides and the
+// occupancy of every attention kernel a bf16 paged call can pick, so that a first call
+// made under capture does no host query of its own.
+extern "C" int fm_static_scratch_init(void) {
+  void *p = nullptr;
+  int rc = static_scratch(&p);
+  if (rc != FM_OK) return rc;
+  DeviceInfo info;
+  rc = device_info(&info);
+  if (rc != FM_OK) return rc;
+  tuning();
+  for (int d : {64, 128})
+    for (int layout : {(int)PAGED16, (int)PAGED})
+      for (int w = 1; w <= NRB_MAX; ++w)
+        for (int qmode : {(int)Q_DIRECT, (int)Q_PACKED})
+          occupancy(select_kernel(layout, d, w, qmode), 64 * (w + 1) * replicas(w));
+  return FM_OK;
+}
+
+extern "C" int fm_tuning_reload(void) {
+  std::call_once(g_tuning_once, read_tuning);
+  read_tuning();
+  return FM_OK;
+}
 
 extern "C" int fm_block_attn_paged_static(
     const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head, void *out,

@@ -155,8 +155,13 @@ int fm_block_attn_paged(
  * it allocates nothing and never synchronizes. A call whose split-KV scratch would exceed
  * the array fails with FM_ERR_WORKSPACE. Every call on one GPU shares that GPU's array:
  * calls that may overlap in time on one GPU (two streams, two threads) race on it. No
- * part of the array has to start cleared (each call writes what it later reads). */
+ * part of the array has to start cleared (each call writes what it later reads). Every
+ * process that loads the library holds the array on each GPU it uses, whether or not it
+ * calls this entry point. Before the first call on a device is captured into a graph,
+ * call fm_static_scratch_init() with that device current (or make one eager call): it
+ * resolves the array's address and fills the host-side caches a first call would query. */
 size_t fm_static_scratch_bytes(void);
+int fm_static_scratch_init(void);
 int fm_block_attn_paged_static(
     const void *q, int64_t q_stride_batch, int64_t q_stride_token, int64_t q_stride_head,
     void *out, int64_t out_stride_batch, int64_t out_stride_token, int64_t out_stride_head,
@@ -452,6 +457,12 @@ int fm_profile_enable(int enable);
  * to follow the clock under sustained load. */
 int fm_clock_probe(uint64_t *out, uint64_t spin_ticks, void *stream);
 int fm_profile_read(double *total_ms, int64_t *launches);
+/* Tuning hook, no reference counterpart: the attention calls read their FLASHMAP_*
+ * overrides (split-KV workgroups and minimum tiles, the small-call kernel's tiles per
+ * share, the query pass, the share cost, the combine's batch) from the environment once,
+ * at the first call; this re-reads them (for tests and sweeps that change them within a
+ * process). Not to be called while another thread launches attention calls. */
+int fm_tuning_reload(void);
 
 #ifdef __cplusplus
 }

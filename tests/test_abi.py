@@ -164,3 +164,8 @@ def test_verify_argument_errors(lib):
     # invalid shapes answer the workspace query with a minimal size
     assert lib.fm_verify_workspace_bytes(4, 17, 30, 8, 128, 0, 1000, 0) == 256
     assert lib.fm_verify_workspace_bytes(4, 17, 32, 8, 96, 0, 1000, 0) == 256
+
+
+def test_tuning_reload(lib):
+    # host only: re-reads the FLASHMAP_* overrides, touches no device
+    assert lib.fm_tuning_reload() == 0

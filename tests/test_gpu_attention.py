@@ -329,7 +329,7 @@ def _tables(kind, rows, d):
 
 @pytest.mark.parametrize("kind", ["interleaved", "cat", "split"])
 @pytest.mark.parametrize("layout", ["contig", "paged"])
-def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
+def test_direct_rows_equal_query_pass(dev, tuning, kind, layout):
     """The attention kernel applies the prologue to the caller's rows itself (direct rows)
     or reads rows a separate query pass normed and rotated: the same bits either way,
     for every rotary table layout, with ragged draft rows (cu_seqlens_q shorter than q_len)."""
@@ -362,10 +362,10 @@ def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
             return o.block_attention_contig(q_pre.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev),
                                             seqlens_k=lens.to(dev), prologue=pro)
     outs = {}
-    monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")  # the persistent kernel (the small-call one reads rows directly)
-    monkeypatch.setenv("FLASHMAP_SHARE_COST", "2")  # one cut of the line for both (their default costs differ)
+    tuning("FLASHMAP_SMALL_TILES", "0")  # the persistent kernel (the small-call one reads rows directly)
+    tuning("FLASHMAP_SHARE_COST", "2")  # one cut of the line for both (their default costs differ)
     for mode in ("1", "0"):
-        monkeypatch.setenv("FLASHMAP_QUERY_PASS", mode)
+        tuning("FLASHMAP_QUERY_PASS", mode)
         outs[mode] = run()
     assert torch.equal(outs["0"], outs["1"]), f"{kind}/{layout}: direct rows differ from the query pass"
     qn = ref.rms_norm_rope_vllm(q_pre[:n_tok], w, table, pos, 1e-6)
@@ -380,7 +380,7 @@ def test_direct_rows_equal_query_pass(dev, monkeypatch, kind, layout):
 
 @pytest.mark.parametrize("layout", ["contig", "paged"])
 @pytest.mark.parametrize("hq,hkv,lens", [(8, 2, [700, 33, 0, 260]), (32, 8, [1100, 5])])
-def test_small_call_kernel(dev, monkeypatch, layout, hq, hkv, lens):
+def test_small_call_kernel(dev, tuning, layout, hq, hkv, lens):
     """Calls whose K/V fits one pass of a few-tile workgroups over the CUs run the small-call
     kernel: against the oracle at 1, 3 and 8 tiles per share and with that kernel off (the
     persistent one), max_seqlen_k far above the lengths (more shares than tiles, so empty
@@ -415,7 +415,7 @@ def test_small_call_kernel(dev, monkeypatch, layout, hq, hkv, lens):
                                             seqlens_k=lens.to(dev), prologue=pro)
     qn = ref.rms_norm_rope_vllm(q_pre[:n_tok], w, table, pos, 1e-6)
     for tiles in ("1", "3", "8", "0"):
-        monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
+        tuning("FLASHMAP_SMALL_TILES", tiles)
         got = run().cpu().view(-1, hq, d)
         print(f"small-call kernel {layout} hq={hq} hkv={hkv} lens={lens.tolist()} tiles per share={tiles}",
               flush=True)
@@ -429,7 +429,7 @@ def test_small_call_kernel(dev, monkeypatch, layout, hq, hkv, lens):
 
 
 @pytest.mark.parametrize("tiles", ["", "1"])
-def test_small_call_fits_the_queried_workspace(dev, monkeypatch, tiles):
+def test_small_call_fits_the_queried_workspace(dev, monkeypatch, tuning, tiles):
     """fm_attn_workspace_bytes covers the small-call kernel at any tiles per share: a
     workspace of exactly the queried size runs the same kernel and split as the pool's
     larger one (identical bits), at C2's shape."""
@@ -439,7 +439,7 @@ def test_small_call_fits_the_queried_workspace(dev, monkeypatch, tiles):
     k = normed_keys(b, hkv, ctx, d, g)
     v = torch.randn(b, hkv, ctx, d, generator=g).bfloat16()
     o = ops()
-    monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
+    tuning("FLASHMAP_SMALL_TILES", tiles)
     pooled = o.block_attention_contig(q.to(dev), k.to(dev), v.to(dev))
     monkeypatch.setattr(o._WORKSPACES, "get",
                         lambda device, nbytes: torch.empty(nbytes, dtype=torch.uint8, device=device))
@@ -449,7 +449,7 @@ def test_small_call_fits_the_queried_workspace(dev, monkeypatch, tiles):
 
 
 @pytest.mark.parametrize("tiles", ["1", "0"])
-def test_lengths_past_max_seqlen_k(dev, monkeypatch, tiles):
+def test_lengths_past_max_seqlen_k(dev, tuning, tiles):
     """Lengths beyond ``max_seqlen_k`` (the caller's bound, used to size the split): the
     shares then hold more tiles than planned (more than the small-call kernel's 8 stages,
     so it walks them in chunks); the results still match the oracle. 0: the persistent
@@ -466,7 +466,7 @@ def test_lengths_past_max_seqlen_k(dev, monkeypatch, tiles):
     cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
     cu = torch.arange(b + 1, dtype=torch.int32) * t
     want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
-    monkeypatch.setenv("FLASHMAP_SMALL_TILES", tiles)
+    tuning("FLASHMAP_SMALL_TILES", tiles)
     got = ops().block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
                                       t, 1, d ** -0.5)
     check_close(got, want)
@@ -474,7 +474,7 @@ def test_lengths_past_max_seqlen_k(dev, monkeypatch, tiles):
 
 @pytest.mark.parametrize("qpass", ["1", "0"])
 @pytest.mark.parametrize("cost", ["0", "1", "3", "6", "40"])
-def test_share_cost_cuts(dev, monkeypatch, cost, qpass):
+def test_share_cost_cuts(dev, tuning, cost, qpass):
     """The persistent kernel cuts its line of tiles into shares by cost (every unit counts
     its tiles plus a fixed cost): at any cost, including one that outweighs the tiles,
     every tile is computed once and every partial merged, for sequences of 0 to 2000
@@ -497,16 +497,16 @@ def test_share_cost_cuts(dev, monkeypatch, cost, qpass):
     want = ref.block_attention_paged_vllm(qn, cache, cu, lens, bt)
     o = ops()
     pro = o.Prologue(w.to(dev), o.rope_from_table(table.to(dev)), pos.to(dev), 1e-6)
-    monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")
-    monkeypatch.setenv("FLASHMAP_SHARE_COST", cost)
-    monkeypatch.setenv("FLASHMAP_QUERY_PASS", qpass)
+    tuning("FLASHMAP_SMALL_TILES", "0")
+    tuning("FLASHMAP_SHARE_COST", cost)
+    tuning("FLASHMAP_QUERY_PASS", qpass)
     got = o.block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
                                   t, lmax, d ** -0.5, prologue=pro)
     check_close(got, want)
 
 
 @pytest.mark.parametrize("qpass", ["1", "0"])
-def test_own_plan_equals_step_plan(dev, monkeypatch, qpass):
+def test_own_plan_equals_step_plan(dev, tuning, qpass):
     """A call given no step plan computes its own (in one extra workgroup of its query pass
     when it has one, else with a launch of its own): the same bits as the call given the
     step plan of ops.attention_plan."""
@@ -522,8 +522,8 @@ def test_own_plan_equals_step_plan(dev, monkeypatch, qpass):
     cache = vllm_cache_from_contig(k, v, lens, page, bt, total).to(dev)
     cu = (torch.arange(b + 1, dtype=torch.int32) * t).to(dev)
     lens_d = lens.to(dev, torch.int32)
-    monkeypatch.setenv("FLASHMAP_SMALL_TILES", "0")
-    monkeypatch.setenv("FLASHMAP_QUERY_PASS", qpass)
+    tuning("FLASHMAP_SMALL_TILES", "0")
+    tuning("FLASHMAP_QUERY_PASS", qpass)
     o = ops()
     own = o.block_attention_paged(q.to(dev), cache, cu, lens_d, bt.to(dev), t, lmax, d ** -0.5)
     step = o.block_attention_paged(q.to(dev), cache, cu, lens_d, bt.to(dev), t, lmax, d ** -0.5,

@@ -189,7 +189,7 @@ def test_paged_fp8_large_batch(dev):
 
 
 @pytest.mark.parametrize("cost", ["0", "1", "4", "40"])
-def test_paged_fp8_share_cost_cuts(dev, monkeypatch, cost):
+def test_paged_fp8_share_cost_cuts(dev, tuning, cost):
     """The e4m3 kernel's line of 64-position tiles cut into shares by cost at any per-unit
     cost (0: by tiles; 40: the cost outweighs the tiles): every tile computed once and
     every partial merged, for sequences of 0 to 3000 positions."""
@@ -203,7 +203,7 @@ def test_paged_fp8_share_cost_cuts(dev, monkeypatch, cost):
     q8 = _e4m3((bs * k_rows, hq, d), g)
     cu = torch.arange(0, bs * k_rows + 1, k_rows, dtype=torch.int32)
     desc = torch.rand(3, bs, hkv, generator=g) + 0.25
-    monkeypatch.setenv("FLASHMAP_SHARE_COST", cost)
+    tuning("FLASHMAP_SHARE_COST", cost)
     got = ops().block_attention_paged_fp8(q8.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
                                           k_rows, 3000, d ** -0.5, descales=desc.to(dev))
     torch.cuda.synchronize()

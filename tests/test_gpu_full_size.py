@@ -79,14 +79,14 @@ def _check_permuted(out, q, cache, cu, lens, bt, hi, fp8):
 
 
 @pytest.mark.parametrize("name", list(CONFIGS))
-def test_full_size_bf16(dev, monkeypatch, name):
+def test_full_size_bf16(dev, tuning, name):
     print(f"full size {name}", flush=True)
     lens, bt, cache, q, cu, hi = _inputs(dev, name)
     out = _run(q, cache, cu, lens, bt, hi, False)
     torch.cuda.synchronize()
     _check_sampled(out, q, cache, lens, bt)
     _check_permuted(out, q, cache, cu, lens, bt, hi, False)
-    monkeypatch.setenv("FLASHMAP_SPLITKV_WORKGROUPS", "61")
+    tuning("FLASHMAP_SPLITKV_WORKGROUPS", "61")
     split = _run(q, cache, cu, lens, bt, hi, False)
     torch.cuda.synchronize()
     check_close(split.cpu().float(), out.cpu().float())

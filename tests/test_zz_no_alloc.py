@@ -77,3 +77,61 @@ def test_static_scratch_too_small_raises(dev):
     assert e.value.code == _native.FM_ERR_WORKSPACE
     torch.cuda.synchronize()
     assert (out == 0).all()  # nothing was launched
+
+
+_CAPTURED_FIRST_CALL = r"""
+import sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from flashmap_amd import ops
+from oracle import attention as ref
+
+dev = torch.device("cuda", 0)
+g = torch.Generator().manual_seed(8)
+D, PAGE, K = 128, 16, 16
+lens = torch.randint(100, 3000, (9,), generator=g)
+pages = [(int(n) + PAGE - 1) // PAGE for n in lens]
+perm = torch.randperm(sum(pages), generator=g)
+bt = torch.zeros(9, max(pages), dtype=torch.int32)
+o = 0
+for b, n in enumerate(pages):
+    bt[b, :n] = perm[o:o + n].int()
+    o += n
+cache = torch.randn(sum(pages), 8, PAGE, 2 * D, generator=g).bfloat16().to(dev)
+q = torch.randn(9 * K, 32, D, generator=g).bfloat16().to(dev)
+pos = torch.cat([int(n) + torch.arange(K) for n in lens]).to(dev)
+pro = ops.Prologue(torch.ones(D, device=dev), ops.rope_from_table(ref.rope_table(3100, D, 1e6).to(dev)), pos, 1e-6)
+cu = (torch.arange(10, dtype=torch.int32) * K).to(dev)
+lens_d, bt_d = lens.to(dev, torch.int32), bt.to(dev)
+args = (q, cache, cu, lens_d, bt_d, K, 3000, D ** -0.5)
+out = torch.zeros_like(q)
+ops.static_scratch_init()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first static call
+    ops.block_attention_paged_static(*args, prologue=pro, out=out)
+want = ops.block_attention_paged(*args, prologue=pro)
+for i in range(3):
+    out.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), f"replay {i} differs from the workspace call"
+    q.mul_(-1.0)  # new queries between replays (eager work), the same shapes
+    want = ops.block_attention_paged(*args, prologue=pro)
+    torch.cuda.synchronize()
+print("captured first call ok", flush=True)
+"""
+
+
+def test_static_first_call_under_capture(dev):
+    """A fresh process whose first fm_block_attn_paged_static call is captured into a HIP
+    graph (after fm_static_scratch_init): every replay equals the workspace call."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    print("static scratch: first call under graph capture, fresh process", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _CAPTURED_FIRST_CALL, root], capture_output=True, text=True,
+                          timeout=110)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-4000:]
+    assert "captured first call ok" in proc.stdout
