@@ -6,10 +6,11 @@ K = 16 draft rows per sequence, batch 64, context lengths drawn uniform in
 [256, 8192] from seed 0, KV paged in 16-token blocks behind a randomly permuted block
 table (vLLM's FlashAttention cache layout), bf16.
 
-One call (one "step") = the QK-RMSNorm + RoPE prologue of the queries (packed per
-unit by its own kernel), the split-KV block attention and the log-sum-exp combine, with
-the step's plan (computed once per step and shared by every layer, like
-FlashAttention's scheduler metadata) prepared before the timed region. Inputs are
+One call (one "step") = two launches: the split-KV block attention, whose consumer
+wavefronts read the caller's query rows and apply the QK-RMSNorm + RoPE prologue
+themselves at each segment start, and the log-sum-exp combine that writes the output
+rows. The step's plan (computed once per step and shared by every layer, like
+FlashAttention's scheduler metadata) is prepared before the timed region. Inputs are
 resident in HBM when timing starts.
 
 Timing: W warm-up calls and K timed calls right after set-up are reported as
@@ -19,8 +20,9 @@ for some milliseconds), then W warm-up calls and exactly K timed calls give `val
 
 Prints one JSON line. `value` is microseconds per call (lower is better); the line
 also carries the achieved HBM bandwidth, a roofline record for the main attention
-kernel (algorithmic bytes / its average duration from HIP events recorded around
-each launch on its stream; `traffic` = the measured HBM bytes per launch from the
+kernel (its own algorithmic bytes -- the call's minus the output rows the combine
+writes -- over its average duration from HIP events recorded around each launch on its
+stream; `call_bytes` = the whole call's; `traffic` = the measured HBM bytes per launch from the
 calibrated FETCH_SIZE / WRITE_SIZE counters committed under profiles/, when present for
 the workload) and the CPU baseline (the oracle on the host cores, on a bounded sample
 of the same workload).
@@ -83,19 +85,50 @@ def build_inputs(name: str, seed: int = 0):
                 q_pre=q_pre, kv_pre=kv_pre, positions=positions, slots=slots, lo=lo, hi=hi)
 
 
+def kernel_source_hash() -> str:
+    """sha256 (16 hex digits) of the attention kernels' sources: counters recorded under
+    profiles/ carry it, and are reported only for the build they were collected on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in ("block_attn.hip", "fm_device.h"):
+        h.update((ROOT / "flashmap_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def traffic_record(name: str, workload: str):
+    """Calibrated HBM bytes per launch of the main kernel from profiles/``name`` (FETCH_SIZE
+    + WRITE_SIZE counters), when recorded for this workload on the kernel sources being
+    timed; None otherwise."""
+    f = ROOT / "profiles" / name
+    if not f.exists():
+        return None
+    rec = json.loads(f.read_text())
+    if rec.get("workload") != workload or rec.get("source_sha") != kernel_source_hash():
+        return None
+    return rec["traffic_bytes"]
+
+
 def mfma_record(workload: str, flops: float, kernel_ms: float, fp8: bool) -> dict:
     """MFMA utilisation of the main kernel: from the rocprofv3 counters committed under
     profiles/ for this workload (SQ_VALU_MFMA_BUSY_CYCLES over the SIMD-cycles of the
-    dispatch), beside the algorithmic FLOPs over the HIP-event duration."""
+    dispatch) when they were collected on the kernel sources being timed (else marked
+    stale), beside the algorithmic FLOPs over the HIP-event duration."""
     rec = {"tflops_algorithmic": round(flops / (kernel_ms * 1e-3) / 1e12, 1),
            "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
            "util_algorithmic": round(flops / (kernel_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
-    name = "attn_fwd_" + workload.split("-", 1)[0] + "_paged_b64" + ("_fp8" if fp8 else "") + ".mfma.json"
+    name = "attn_fwd_" + workload.split("-", 1)[0] + "_paged_b" + workload.rsplit("-b", 1)[1].split("-")[0] \
+        + ("_fp8" if fp8 else "") + ".mfma.json"
     f = ROOT / "profiles" / name
     if f.exists():
         c = json.loads(f.read_text())
         if c.get("workload") == workload:
-            rec.update({"util": c["util"], "source": f"profiles/{name}", "counters": c["counters"]})
+            rec.update({"source": f"profiles/{name}", "counters": c["counters"]})
+            if c.get("source_sha") == kernel_source_hash():
+                rec["util"] = c["util"]
+            else:
+                rec.update({"util": None, "stale": True, "util_recorded": c["util"],
+                            "note": "counters recorded on other kernel sources than the ones timed"})
     return rec
 
 
@@ -120,7 +153,9 @@ def algorithmic_bytes(inp, kv_bytes: int = 2) -> dict:
     meta = 8 * batch
     rope = batch * k_rows * d * 4
     flops = 4 * k_rows * hq * d * sum_l
-    return dict(kv=kv, total=kv + qo + table + meta + rope, flops=flops, sum_l=sum_l)
+    total = kv + qo + table + meta + rope
+    # the main kernel's own share: everything but the output rows, which the combine writes
+    return dict(kv=kv, total=total, kernel=total - qo // 2, flops=flops, sum_l=sum_l)
 
 
 def cpu_paged_cache(inp, table) -> torch.Tensor:
@@ -141,15 +176,57 @@ def cpu_paged_cache(inp, table) -> torch.Tensor:
     return cache
 
 
+def cpu_model() -> str:
+    """The host CPU's model string (``/proc/cpuinfo``)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_timed(run, weights: list, unit: str, what: str, budget_s: float, threads: int | None = None,
+              warmups: int = 2, calls: int = 5) -> dict:
+    """The CPU baseline's protocol: ``run(n)`` does the call's work for its first ``n``
+    items (sequences, requests, rows), ``weights[i]`` is item i's share of the work (context
+    positions, rows). One probe of the first item prices the work; the sample is the
+    longest prefix whose call fits ``budget_s / (warmups + calls)``; then ``warmups``
+    untimed calls of the sample and the median of ``calls`` timed ones, scaled to the
+    whole call by weight."""
+    cores = threads or len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t0 = time.perf_counter()
+    run(1)
+    per_weight = (time.perf_counter() - t0) / max(weights[0], 1)
+    per_call = budget_s / (warmups + calls)
+    n, acc = 0, 0.0
+    while n < len(weights) and (n == 0 or (acc + weights[n]) * per_weight <= per_call):
+        acc += weights[n]
+        n += 1
+    for _ in range(warmups):
+        run(n)
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        run(n)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    total = sum(weights)
+    return {"value": round(med * total / acc * 1e6, 1), "unit": unit, "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"first {n} of {len(weights)} {what} ({int(acc)} of {int(total)} by weight): median of "
+                      f"{calls} calls after {warmups} warm-ups, scaled to the whole call by weight"}
+
+
 def cpu_baseline(inp, budget_s: float = 12.0) -> dict:
     """The oracle (fp32 torch on the host cores) on the call's work: per sequence, the
-    Q prologue, the block-table gather of K/V from the paged cache, then attention.
-    Sequences run in order until the time budget is spent; the time is scaled to the
-    whole call by context positions."""
+    Q prologue, the block-table gather of K/V from the paged cache, then attention
+    (``cpu_timed``'s protocol, weighted by context positions)."""
     from oracle import attention as ref
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     d, k_rows = inp["d"], inp["k_rows"]
     table = ref.rope_table(inp["hi"] + k_rows + 1, d, 1e6)
     w = torch.ones(d)
@@ -163,26 +240,13 @@ def cpu_baseline(inp, budget_s: float = 12.0) -> dict:
         qn = ref.rms_norm_rope_vllm(q, w, table, n + torch.arange(k_rows), 1e-6)
         return ref.attention(qn.transpose(0, 1), k, v)
 
-    one(0)  # warm-up
-    t0 = time.perf_counter()
-    done_l = 0
-    done = 0
-    for b in range(inp["batch"]):
-        one(b)
-        done_l += int(lens[b])
-        done += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    elapsed = time.perf_counter() - t0
-    scale = int(lens.sum()) / done_l
-    return {
-        "value": round(elapsed * scale * 1e6, 1),
-        "unit": "us/call",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"first {done} of {inp['batch']} sequences ({done_l} of {int(lens.sum())} context "
-                  f"positions): fp32 oracle Q prologue + block-table gather + attention, scaled by positions",
-    }
+    def run(count):
+        for b in range(count):
+            one(b)
+
+    rec = cpu_timed(run, [int(n) for n in lens], "us/call", "sequences", budget_s)
+    rec["sample"] += " (context positions); fp32 oracle Q prologue + block-table gather + attention"
+    return rec
 
 
 # The drafter workloads onto an e4m3 (fp8) paged cache: name -> the bf16 workload whose
@@ -274,18 +338,20 @@ def run_select(args, dev) -> dict:
     if not args.no_cpu_baseline:
         from oracle import sampling as S
 
-        cores = len(os.sched_getaffinity(0))
-        n = 16
-        x = logits[:n].float().cpu().numpy()
-        t0 = time.perf_counter()
-        if mode == "argmax":
-            S.split_argmax(x)
-        else:
-            S.sample_rows(x, temps[:n].cpu().numpy(), greedy[:n].cpu().numpy(), 1)
-        el = time.perf_counter() - t0
-        result["cpu_baseline"] = {"value": round(el * rows / n * 1e6, 1), "unit": "us/call", "cores": 1,
-                                  "kind": "port", "sample": f"first {n} of {rows} rows, numpy oracle, "
-                                                            "scaled by rows"}
+        x = logits[:64].float().cpu().numpy()
+        tc, gc = temps[:64].cpu().numpy(), greedy[:64].cpu().numpy()
+
+        def run(n):
+            if mode == "argmax":
+                S.split_argmax(x[:n])
+            else:
+                S.sample_rows(x[:n], tc[:n], gc[:n], 1)
+
+        weights = [1] * rows  # the sample is at most the 64 rows copied to the host
+        rec = cpu_timed(lambda n: run(min(n, 64)), weights[:64], "us/call", "rows", args.cpu_budget, threads=1)
+        rec["value"] = round(rec["value"] * rows / 64, 1)
+        rec["sample"] += f", of the first 64 of {rows} rows (scaled by rows); numpy oracle, one thread"
+        result["cpu_baseline"] = rec
     return result
 
 
@@ -336,47 +402,28 @@ def _flushed(call, args, dev, flush_mb: int = 512) -> dict:
             "kernel_ms": tot.value / max(cnt.value, 1)}
 
 
-# The vLLM plugin's one-jump draft step (flashmap_amd.draft_step.DraftStep): name ->
-# (requests, ctx lo, ctx hi, drafter config overrides). The released 8B drafter's shape
+# The vLLM plugin's draft step (flashmap_amd.draft_step.DraftStep): name -> (requests,
+# ctx lo, ctx hi, jumps, drafter config overrides). The released 8B drafter's shape
 # (hidden 2048, 16 heads of 128, 6 layers, GELU MLP 8192) over a Qwen3-8B target (hidden
-# 4096, vocabulary 151936); contexts drawn as C3's, paged in 16-token blocks.
+# 4096, vocabulary 151936); contexts drawn as C3's, paged in 16-token blocks. Two jumps
+# (Algorithm 8) carry a state over the whole vocabulary between them and run the DiT, and
+# so every layer's cross-attention, twice.
 DRAFT_STEP_WORKLOADS = {
-    "draft-step-8b-b64": (64, 256, 8192, {}),
+    "draft-step-8b-b64": (64, 256, 8192, 1, {}),
+    "draft-step-8b-b64-2jump": (64, 256, 8192, 2, {}),
 }
 
 
-def _draft_weights(step) -> dict:
-    """The oracle's plain-tensor view of a prepared DraftStep (on the CPU)."""
-    m, cpu = step.model, (lambda t: t.detach().cpu())
-    w = {"embed": cpu(step.embed_weight), "anchor_proj.weight": cpu(m.anchor_proj.weight),
-         "anchor_proj.bias": cpu(m.anchor_proj.bias), "anchor_norm.weight": cpu(m.anchor_norm.weight),
-         "anchor_norm.eps": m.anchor_norm.eps, "context_kv_weight": cpu(step.context_kv_weight),
-         "context_k_norm": cpu(step.context_k_norm), "k_eps": step.k_eps, "cos_sin": cpu(step.cos_sin),
-         "heads": step.heads, "block": step.block, "noise_eigvals": cpu(step.noise_eigvals),
-         "noise_embed": cpu(step.noise_embed), "noise_eps": step.noise_eps, "gain": step.noise_gain,
-         "first_hidden": cpu(step.first_hidden), "ln_eps": m.final_adaln.eps,
-         "final_mod": [cpu(t) for t in step.final_mod], "head_weight": cpu(step.head_weight),
-         "head_bias": cpu(step.head_bias), "layers": []}
-    for i, layer in enumerate(m.layers):
-        lw = {"mods": [[cpu(t) for t in mod] for mod in step.layer_mods[i]], "self_qkv": cpu(step.self_qkv[i]),
-              "self_q_norm": cpu(layer.self_attn.q_norm.weight), "self_k_norm": cpu(layer.self_attn.k_norm.weight),
-              "qk_eps": layer.self_attn.q_norm.eps, "self_o": cpu(layer.self_attn.o_proj.weight),
-              "cross_q": cpu(layer.cross_attn.q_proj.weight), "cross_q_norm": cpu(layer.cross_attn.q_norm.weight),
-              "cross_o": cpu(layer.cross_attn.o_proj.weight)}
-        lw.update({k: cpu(v) for k, v in layer.mlp.state_dict().items()})
-        w["layers"].append(lw)
-    return w
-
-
 def run_draft_step(args, dev) -> dict:
-    """One call = one draft step for the batch: the anchors' context rows written, the
-    folded noise read-out, 6 DiT layers (each with its cross-attention over its paged
-    cache), the folded head over the vocabulary and the greedy argmax. The plan is built
-    per step inside the call."""
+    """One call = one draft step for the batch: the anchors' context rows written, then
+    per jump the DiT input (one jump: the folded noise read-out; several: the state's
+    embedding), 6 DiT layers (each with its cross-attention over its paged cache) and,
+    between jumps, the state's update; then the folded head over the vocabulary and the
+    greedy argmax. The plan is built per step inside the call."""
     from flashmap_amd import drafter as d
     from flashmap_amd.draft_step import DraftStep
 
-    batch, lo, hi, over = DRAFT_STEP_WORKLOADS[args.workload]
+    batch, lo, hi, jumps, over = DRAFT_STEP_WORKLOADS[args.workload]
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(lo, hi + 1, (batch,), generator=g)  # C3's draw: context positions incl. the anchor
     page = 16
@@ -394,7 +441,7 @@ def run_draft_step(args, dev) -> dict:
     gd = torch.Generator(device=dev).manual_seed(0)
     embed = torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=gd, device=dev).bfloat16()
     lm_head = (torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=gd, device=dev) / 64).bfloat16()
-    step = DraftStep(model, embed, lm_head, max_model_len=hi + cfg.block_size + 1)
+    step = DraftStep(model, embed, lm_head, max_model_len=hi + cfg.block_size + 1, num_steps=jumps)
     heads, hd = step.heads, step.head_dim
     caches = []
     for _ in model.layers:
@@ -405,7 +452,7 @@ def run_draft_step(args, dev) -> dict:
     anchors = torch.randint(0, cfg.vocab_size, (batch,), generator=g).to(dev)
     a_pos = (lens - 1).to(dev)
     a_slots = (bt[torch.arange(batch), (lens - 1) // page].long() * page + (lens - 1) % page).to(dev)
-    z = torch.randn(batch * cfg.block_size, cfg.target_hidden_size, generator=gd, device=dev)
+    z = torch.randn(batch * cfg.block_size, step.noise_columns, generator=gd, device=dev)
     bt_d = bt.to(dev)
     tokens = torch.empty(batch * cfg.block_size, dtype=torch.int64, device=dev)
 
@@ -418,65 +465,202 @@ def run_draft_step(args, dev) -> dict:
     k_rows, layers = cfg.block_size, len(model.layers)
     attn_bytes = sum_l * heads * hd * 2 * 2 + 2 * batch * k_rows * heads * hd * 2 + 4 * total + 8 * batch \
         + batch * k_rows * hd * 4
-    gbs = attn_bytes / (kernel_ms * 1e-3) / 1e9
+    attn_own = attn_bytes - batch * k_rows * heads * hd * 2  # the combine writes the output rows
+    gbs = attn_own / (kernel_ms * 1e-3) / 1e9
     dim, inter, th, vocab = cfg.hidden_size, cfg.intermediate_size, cfg.target_hidden_size, cfg.vocab_size
     rows = batch * k_rows
-    gemm_flops = 2 * rows * (layers * (3 * dim * dim + 3 * dim * dim + 2 * dim * inter) + vocab * dim + th * dim) \
-        + 2 * batch * (th * dim + 2 * layers * dim * dim)
+    dit_flops = 2 * rows * layers * (6 * dim * dim + 2 * dim * inter)
+    if jumps == 1:  # the folded noise read-out
+        entry_flops = 2 * rows * th * dim
+    else:  # per jump the state's two projections onto the embedding and x_embed; the jump head between
+        entry_flops = jumps * (2 * 2 * rows * vocab * th + 2 * rows * th * dim) + (jumps - 1) * 2 * rows * dim * vocab
+    gemm_flops = jumps * dit_flops + entry_flops + 2 * rows * vocab * dim + 2 * batch * (th * dim + 2 * layers * dim * dim)
     result = {
-        "metric": "one-jump draft step µs/step (anchor write, noise read-out, 6 DiT layers, folded head, argmax), "
-                  "8B drafter, K=16, batch 64, ctx 256–8k, 1 GPU",
+        "metric": f"{jumps}-jump draft step µs/step (anchor write, " + (
+            "noise read-out" if jumps == 1 else "state embedding and update") + f", {jumps} x 6 DiT layers, "
+                  "folded head, argmax), 8B drafter, K=16, batch 64, ctx 256–8k, 1 GPU",
         "value": round(ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic: random-init drafter and target embedding / LM head, random paged K/V, "
                                  "seeded draw of lengths and block table (C3's)",
-        "config": {"workload": args.workload, "batch": batch, "hidden": dim, "heads": heads, "head_dim": hd,
-                   "layers": layers, "intermediate": inter, "mlp": cfg.mlp_type, "vocab": vocab,
+        "config": {"workload": args.workload, "batch": batch, "jumps": jumps, "hidden": dim, "heads": heads,
+                   "head_dim": hd, "layers": layers, "intermediate": inter, "mlp": cfg.mlp_type, "vocab": vocab,
                    "target_hidden": th, "block_queries": k_rows, "ctx_lo": lo, "ctx_hi": hi, "ctx_sum": sum_l,
                    "page": page},
         "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel (the step's cross-attention, one launch per layer)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": attn_bytes,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": attn_own,
+                     "call_bytes": attn_bytes,
+                     "kernel_us": round(kernel_ms * 1e3, 2)},
+        "attention_share": round(jumps * layers * kernel_ms / ms, 4),
+        "gemm_tflop_per_step": round(gemm_flops / 1e12, 4),
+        **_timing_fields(timing),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = draft_step_cpu_baseline(step, lm_head, lens, anchors.cpu(), z.cpu(), args.cpu_budget)
+    return result
+
+
+def draft_step_cpu_baseline(step, lm_head, lens, anchors, z, budget_s) -> dict:
+    """The draft-step oracle (bf16/fp32 torch on the host cores, prepared from the
+    drafter's raw weights) request by request, each over a CPU paged cache of its own
+    context (random values: the time does not depend on them); ``cpu_timed``'s protocol,
+    weighted by requests."""
+    from oracle import draft_step as oracle
+
+    model = step.model
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    w = oracle.prepare(sd, dict(vars(model.config)), step.embed_weight.cpu(), lm_head.cpu(), None, step.num_steps,
+                       int(lens.max()) + step.block + 1)
+    k, page = step.block, 16
+    g = torch.Generator().manual_seed(1)
+    held = {}
+
+    def request(b):
+        if b not in held:  # set-up, outside the timed calls after the first
+            n = int(lens[b])
+            blocks = math.ceil(n / page)
+            held[b] = ([torch.randn(blocks, step.heads, page, 2 * step.head_dim, generator=g).bfloat16()
+                        for _ in model.layers], torch.arange(blocks, dtype=torch.int32)[None],
+                       torch.tensor([n - 1]))
+        return held[b]
+
+    def run(count):
+        for b in range(count):
+            caches, bt, pos = request(b)
+            oracle.write_anchors(w, anchors[b:b + 1], pos, pos.clone(), caches, page)
+            if step.num_steps == 1:  # the noise through the embedding (its values do not change the time)
+                oracle.draft(w, pos, caches, bt, noise_embeds=z[b * k:(b + 1) * k].bfloat16())[1].argmax(-1)
+            else:
+                oracle.draft(w, pos, caches, bt, state=z[b * k:(b + 1) * k])[1].argmax(-1)
+
+    rec = cpu_timed(run, [1] * len(lens), "us/step", "requests", budget_s)
+    rec["sample"] += "; the oracle's anchor write, DiT input, DiT per jump and head + LM head + argmax"
+    return rec
+
+
+# The SGLang plugin's one-jump draft step (flashmap_amd.sglang_step.SGLangDraftStep): name
+# -> (requests, candidates per request, ctx lo, ctx hi). The 8B drafter over a Qwen3-8B
+# target as for the vLLM step; each layer's context in an SGLang token pool at randomly
+# permuted rows. With candidates (tree drafting) a request's blocks attend together to its
+# one context.
+SGLANG_STEP_WORKLOADS = {
+    "sglang-draft-step-8b-b64": (64, 1, 256, 8192),
+    "sglang-draft-step-8b-b4-n8": (4, 8, 1024, 8192),
+}
+
+
+def run_sglang_step(args, dev) -> dict:
+    """One call = one SGLang draft step: the anchors' pool rows written, the folded noise
+    read-out, 6 DiT layers (each with its token-paged cross-attention), the folded head
+    and the sampler (every row greedy). The plan is built per step inside the call."""
+    from flashmap_amd import drafter as d
+    from flashmap_amd.sglang_step import SGLangDraftStep
+
+    requests, n_cand, lo, hi = SGLANG_STEP_WORKLOADS[args.workload]
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(lo, hi + 1, (requests,), generator=g)  # context positions incl. the anchor
+    ctx = int(lens.sum())
+    slots = torch.randperm(ctx, generator=g).to(torch.int32)
+    page_table = torch.zeros(requests, hi, dtype=torch.int32)
+    o = 0
+    for r in range(requests):
+        page_table[r, :int(lens[r])] = slots[o:o + int(lens[r])]
+        o += int(lens[r])
+    torch.manual_seed(0)
+    model = d.FlashMapDraftModel(d.drafter_config()).to(dev, torch.bfloat16)
+    cfg = model.config
+    gd = torch.Generator(device=dev).manual_seed(0)
+    embed = torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=gd, device=dev).bfloat16()
+    lm_head = (torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=gd, device=dev) / 64).bfloat16()
+    step = SGLangDraftStep(model, embed, lm_head, max_positions=hi + cfg.block_size + 1)
+    heads, hd, k = step.heads, step.head_dim, cfg.block_size
+    k_bufs, v_bufs = [], []
+    for _ in model.layers:
+        for bufs in (k_bufs, v_bufs):
+            b = torch.empty(ctx, heads, hd, dtype=torch.bfloat16, device=dev)
+            b.normal_(generator=gd)
+            bufs.append(b)
+    meta = step.pool_meta(k_bufs, v_bufs)
+    anchors = torch.randint(0, cfg.vocab_size, (requests,), generator=g).to(dev)
+    a_pos = (lens - 1).to(dev)
+    a_locs = page_table[torch.arange(requests), lens - 1].long().to(dev)
+    rows = requests * n_cand * k
+    z = torch.randn(rows, cfg.target_hidden_size, generator=gd, device=dev)
+    pt = page_table.to(dev)
+    temps = torch.ones(rows, device=dev)
+    greedy = torch.ones(rows, dtype=torch.bool, device=dev)
+    seed = torch.tensor(7, dtype=torch.int64, device=dev)
+    tokens = torch.empty(rows, dtype=torch.int64, device=dev)
+
+    def call():
+        hidden = step(anchors, a_pos, a_locs, z, k_bufs, v_bufs, pt, n_cand=n_cand, meta=meta)
+        tokens.copy_(step.sample(hidden, temps, greedy, seed))
+
+    timing = _measure(call, args)
+    ms, kernel_ms = timing["ms"], timing["kernel_ms"]
+    layers = len(model.layers)
+    own = ctx * heads * hd * 2 * 2 + 4 * ctx + 4 * requests + rows * heads * hd * 2  # K/V, rows, lengths, Q
+    gbs = own / (kernel_ms * 1e-3) / 1e9
+    dim, inter, th, vocab = cfg.hidden_size, cfg.intermediate_size, cfg.target_hidden_size, cfg.vocab_size
+    gemm_flops = 2 * rows * (layers * (6 * dim * dim + 2 * dim * inter) + th * dim + vocab * dim) \
+        + 2 * requests * (th * dim + 2 * layers * dim * dim)
+    result = {
+        "metric": f"SGLang one-jump draft step µs/step ({n_cand} candidate(s) per request: anchor write, noise "
+                  "read-out, 6 DiT layers, folded head, sampler), 8B drafter, 1 GPU",
+        "value": round(ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: random-init drafter and target embedding / LM head, random pools, "
+                                 "seeded draw of lengths and pool rows",
+        "config": {"workload": args.workload, "requests": requests, "candidates": n_cand, "hidden": dim,
+                   "heads": heads, "head_dim": hd, "layers": layers, "intermediate": inter, "mlp": cfg.mlp_type,
+                   "vocab": vocab, "target_hidden": th, "block_queries": k, "ctx_lo": lo, "ctx_hi": hi,
+                   "ctx_sum": ctx, "layout": "sglang token pools (pool, heads, head_dim), page table"},
+        "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel (the step's cross-attention, one launch per layer)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": own,
                      "kernel_us": round(kernel_ms * 1e3, 2)},
         "attention_share": round(layers * kernel_ms / ms, 4),
         "gemm_tflop_per_step": round(gemm_flops / 1e12, 4),
         **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = draft_step_cpu_baseline(step, lens, anchors.cpu(), z.cpu(), args.cpu_budget)
+        result["cpu_baseline"] = sglang_step_cpu_baseline(step, lm_head, lens, anchors.cpu(), n_cand, args.cpu_budget)
     return result
 
 
-def draft_step_cpu_baseline(step, lens, anchors, z, budget_s) -> dict:
-    """The draft-step oracle (fp32/bf16 torch on the host cores) request by request, each
-    over a CPU paged cache of its own context (random values: the time does not depend on
-    them), until the budget is spent; scaled to the batch by requests."""
+def sglang_step_cpu_baseline(step, lm_head, lens, anchors, n_cand, budget_s) -> dict:
+    """The SGLang step's oracle (bf16/fp32 torch on the host cores, prepared from the
+    drafter's raw weights) request by request over a pool of its own context (random
+    values); ``cpu_timed``'s protocol, weighted by requests."""
     from oracle import draft_step as oracle
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    w = _draft_weights(step)
-    k, page = step.block, 16
+    model = step.model
+    sd = {key: v.detach().cpu() for key, v in model.state_dict().items()}
+    w = oracle.prepare(sd, dict(vars(model.config)), step.embed_weight.cpu(), lm_head.cpu(), None, 1,
+                       int(lens.max()) + step.block + 1)
+    k = step.block
     g = torch.Generator().manual_seed(1)
-    done, t_used = 0, 0.0
-    for b in range(len(lens)):
-        n = int(lens[b])
-        blocks = math.ceil(n / page)
-        caches = [torch.randn(blocks, step.heads, page, 2 * step.head_dim, generator=g).bfloat16()
-                  for _ in step.model.layers]
-        bt = torch.arange(blocks, dtype=torch.int32)[None]
-        pos = torch.tensor([n - 1])
-        t0 = time.perf_counter()
-        oracle.write_anchor_rows(w, anchors[b:b + 1], pos, pos.clone(), caches, page)
-        hidden = oracle.one_jump(w, anchors[b:b + 1], pos, z[b * k:(b + 1) * k], caches, bt)
-        oracle.draft_logits(w, hidden).argmax(-1)
-        t_used += time.perf_counter() - t0
-        done += 1
-        if t_used > budget_s:
-            break
-    return {"value": round(t_used / done * len(lens) * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
-            "sample": f"first {done} of {len(lens)} requests: the oracle's anchor write, read-out, DiT and folded "
-                      "head + argmax, scaled by requests"}
+    held = {}
+
+    def request(r):
+        if r not in held:
+            n = int(lens[r])
+            held[r] = ([torch.randn(n, step.heads, step.head_dim, generator=g).bfloat16() for _ in model.layers],
+                       [torch.randn(n, step.heads, step.head_dim, generator=g).bfloat16() for _ in model.layers],
+                       torch.arange(n, dtype=torch.int32)[None], torch.tensor([n - 1]),
+                       torch.randn(n_cand * k, step.cfg.target_hidden_size, generator=g).bfloat16())
+        return held[r]
+
+    def run(count):
+        for r in range(count):
+            kb, vb, pt, pos, noise = request(r)
+            oracle.pool_write_anchors(w, anchors[r:r + 1], pos, pos.clone(), kb, vb)
+            oracle.pool_draft(w, pos, kb, vb, pt, noise, n_cand)[1].argmax(-1)
+
+    rec = cpu_timed(run, [1] * len(lens), "us/step", "requests", budget_s)
+    rec["sample"] += "; the oracle's anchor write, read-out, DiT over token pools and head + LM head + argmax"
+    return rec
 
 
 # The batch-1 contiguous case (FlashMapCache views): name -> (batch, hq, hkv, head_dim, K,
@@ -516,7 +700,8 @@ def run_contig(args, dev) -> dict:
     ms, kernel_ms = t["ms"], t["kernel_ms"]
     kv = batch * hkv * ctx * d * 2 * 2
     total = kv + 2 * batch * k_rows * hq * d * 2 + batch * k_rows * d * 4
-    gbs = total / (kernel_ms * 1e-3) / 1e9
+    own = total - batch * k_rows * hq * d * 2  # the merge writes the output rows
+    gbs = own / (kernel_ms * 1e-3) / 1e9
     result = {
         "metric": METRIC.replace("batch 64, ctx 256–8k", f"batch {batch}, ctx {ctx} contiguous"),
         "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -527,7 +712,8 @@ def run_contig(args, dev) -> dict:
                    "prologue": "QK-RMSNorm + RoPE inside the attention kernel (no query pass), "
                                "one (cos, sin) row per draft token as FlashMapAttention passes them"},
         "roofline": {"bound": "hbm", "kernel": "attn_small_kernel", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": total,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": own,
+                     "call_bytes": total,
                      "kernel_us": round(kernel_ms * 1e3, 2)},
         "warm_us_per_call": round(t["warm_ms"] * 1e3, 2),
         "graph_us_per_call": round(t["graph_ms"] * 1e3, 2),
@@ -537,15 +723,14 @@ def run_contig(args, dev) -> dict:
                   "kernel, after a flush",
     }
     if not args.no_cpu_baseline:
-        cores = len(os.sched_getaffinity(0))
-        torch.set_num_threads(cores)
-        t0 = time.perf_counter()
-        for b in range(batch):
-            qn = ref.rms_norm_rope_vllm(q[b], w, table, qpos[b * k_rows:(b + 1) * k_rows], 1e-6)
-            ref.attention(qn.transpose(0, 1), keys[b], values[b])
-        el = time.perf_counter() - t0
-        result["cpu_baseline"] = {"value": round(el * 1e6, 1), "unit": "us/call", "cores": cores, "kind": "port",
-                                  "sample": f"all {batch} sequence(s): fp32 oracle prologue + attention"}
+        def run(count):
+            for b in range(count):
+                qn = ref.rms_norm_rope_vllm(q[b], w, table, qpos[b * k_rows:(b + 1) * k_rows], 1e-6)
+                ref.attention(qn.transpose(0, 1), keys[b], values[b])
+
+        rec = cpu_timed(run, [ctx] * batch, "us/call", "sequences", args.cpu_budget)
+        rec["sample"] += "; fp32 oracle prologue + attention"
+        result["cpu_baseline"] = rec
     return result
 
 
@@ -707,10 +892,11 @@ def run_tree(args, dev) -> dict:
     kv = ctx * hkv * d * 2 * (1 if fp8 else 2)
     total = kv + 4 * ctx + 4 * requests + 2 * requests * q_len * hq * d * 2
     flops = 4 * q_len * hq * d * ctx
-    gbs = total / (kernel_ms * 1e-3) / 1e9
+    own = total - requests * q_len * hq * d * 2  # the combine writes the output rows
+    gbs = own / (kernel_ms * 1e-3) / 1e9
     tflops = flops / (kernel_ms * 1e-3) / 1e12
     hbm_frac, mfma_frac = gbs / HBM_PEAK_GBS, tflops / MFMA_BF16_PEAK_TFLOPS
-    mfma_bound = flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) > total / (HBM_PEAK_GBS * 1e9)
+    mfma_bound = flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) > own / (HBM_PEAK_GBS * 1e9)
     result = {
         "metric": "tree-drafting cross-attn µs/call, n_cand x 16 rows per request, 1 GPU",
         "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -727,7 +913,8 @@ def run_tree(args, dev) -> dict:
                       "frac": round(hbm_frac, 4)}),
         "hbm_frac": round(hbm_frac, 4), "mfma_frac": round(mfma_frac, 4),
     }
-    result["roofline"].update({"kernel": "attn_fwd_kernel", "traffic": None, "bytes_per_launch": total,
+    result["roofline"].update({"kernel": "attn_fwd_kernel", "traffic": None, "bytes_per_launch": own,
+                               "call_bytes": total,
                                "flops_per_launch": flops, "kernel_us": round(kernel_ms * 1e3, 2)})
     result.update(_timing_fields(timing))
     if not args.no_cpu_baseline:
@@ -740,27 +927,21 @@ def tree_cpu_baseline(q, kb, vb, lens, pt, budget_s, fp8: bool = False) -> dict:
     request until the budget is spent, scaled to the whole call by context positions."""
     from oracle import attention as ref
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     kc, vc, qc = kb.cpu(), vb.cpu(), q.cpu()
     if fp8:  # widened once (exact): the oracle would widen the whole pool for every request
         kc, vc = kc.float(), vc.float()
-    done_l = done = 0
-    t0 = time.perf_counter()
-    for b in range(len(lens)):
-        if fp8:
-            ref.block_attention_token_paged_fp8(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
-        else:
-            ref.block_attention_token_paged(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
-        done_l += int(lens[b])
-        done += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    elapsed = time.perf_counter() - t0
-    return {"value": round(elapsed * int(lens.sum()) / done_l * 1e6, 1), "unit": "us/call", "cores": cores,
-            "kind": "port", "sample": f"first {done} of {len(lens)} requests ({done_l} context positions): "
-                                      f"fp32 oracle token-paged{' e4m3 (pools widened to fp32 once)' if fp8 else ''} "
-                                      "attention, scaled by positions"}
+
+    def run(count):
+        for b in range(count):
+            if fp8:
+                ref.block_attention_token_paged_fp8(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
+            else:
+                ref.block_attention_token_paged(qc[b:b + 1], kc, vc, lens[b:b + 1], pt[b:b + 1])
+
+    rec = cpu_timed(run, [int(n) for n in lens], "us/call", "requests", budget_s)
+    rec["sample"] += (f" (context positions); fp32 oracle token-paged"
+                      f"{' e4m3 (pools widened to fp32 once)' if fp8 else ''} attention")
+    return rec
 
 
 def run_verify(args, dev) -> dict:
@@ -802,13 +983,12 @@ def run_verify(args, dev) -> dict:
     ms, kernel_ms, timing = _time_call(call, args)
     kv = ctx * hkv * d * 2 * 2
     total = kv + 4 * ctx + 4 * (batch + 1) + 2 * batch * length * hq * d * 2 + batch * length * hkv * d * 2 * 2
-    achieved = total / (kernel_ms * 1e-3) / 1e9
-    traffic = None
-    tfile = ROOT / "profiles" / f"attn_fwd_{args.workload.replace('-qwen3-8b-', '_').replace('-', '_')}.traffic.json"
-    if tfile.exists():
-        rec = json.loads(tfile.read_text())
-        if rec.get("workload") == args.workload:
-            traffic = rec["traffic_bytes"]
+    # the main kernel's own share: the context and the query rows (the query pass reads the
+    # verify tokens' K/V, the combine writes the output rows)
+    own = kv + 4 * ctx + 4 * (batch + 1) + batch * length * hq * d * 2
+    achieved = own / (kernel_ms * 1e-3) / 1e9
+    traffic = traffic_record(f"attn_fwd_{args.workload.replace('-qwen3-8b-', '_').replace('-', '_')}.traffic.json",
+                             args.workload)
     result = {
         "metric": "target verify attn µs/call + achieved HBM TB/s, 17 verify tokens, batch 64, ctx 256–8k, 1 GPU",
         "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -820,7 +1000,8 @@ def run_verify(args, dev) -> dict:
         "hbm_tbs": round(total / (ms * 1e-3) / 1e12, 3),
         "roofline": {"bound": "hbm", "kernel": "attn_fwd_kernel", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "bytes_per_launch": total, "kernel_us": round(kernel_ms * 1e3, 2)},
+                     "traffic": traffic, "bytes_per_launch": own, "call_bytes": total,
+                     "kernel_us": round(kernel_ms * 1e3, 2)},
         **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
@@ -834,28 +1015,23 @@ def verify_cpu_baseline(q, k_ext, v_ext, kb, vb, indptr, indices, cmask, mask, l
     spent, scaled to the whole call by context positions."""
     from oracle import attention as ref
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     ip, idx = indptr.cpu(), indices.cpu()
-    done_l = done = 0
-    t0 = time.perf_counter()
-    for b in range(len(lens)):
-        lo_, hi_ = int(ip[b]), int(ip[b + 1])
-        rows = idx[lo_:hi_].long()
-        sub_ip = torch.tensor([0, hi_ - lo_], dtype=torch.int32)
-        tok = slice(b * length, (b + 1) * length)
-        sub_mask = None if cmask is None else cmask.cpu()[b * length * length:(b + 1) * length * length]
-        ref.verify_attention(q[tok].cpu(), k_ext[tok].cpu(), v_ext[tok].cpu(), kb[rows.to(kb.device)].cpu(),
-                             vb[rows.to(vb.device)].cpu(), sub_ip, torch.arange(hi_ - lo_), sub_mask, None,
-                             mask == "qlen")
-        done_l += hi_ - lo_
-        done += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    elapsed = time.perf_counter() - t0
-    return {"value": round(elapsed * int(lens.sum()) / done_l * 1e6, 1), "unit": "us/call", "cores": cores,
-            "kind": "port", "sample": f"first {done} of {len(lens)} requests ({done_l} context positions): "
-                                      "fp32 oracle verify attention, scaled by positions"}
+    kh, vh, qh, keh, veh = kb.cpu(), vb.cpu(), q.cpu(), k_ext.cpu(), v_ext.cpu()
+    mh = None if cmask is None else cmask.cpu()
+
+    def run(count):
+        for b in range(count):
+            lo_, hi_ = int(ip[b]), int(ip[b + 1])
+            rows = idx[lo_:hi_].long()
+            sub_ip = torch.tensor([0, hi_ - lo_], dtype=torch.int32)
+            tok = slice(b * length, (b + 1) * length)
+            sub_mask = None if mh is None else mh[b * length * length:(b + 1) * length * length]
+            ref.verify_attention(qh[tok], keh[tok], veh[tok], kh[rows], vh[rows], sub_ip, torch.arange(hi_ - lo_),
+                                 sub_mask, None, mask == "qlen")
+
+    rec = cpu_timed(run, [int(n) for n in lens], "us/call", "requests", budget_s)
+    rec["sample"] += " (context positions); fp32 oracle verify attention (pool rows gathered on the host)"
+    return rec
 
 
 def main() -> int:
@@ -867,7 +1043,7 @@ def main() -> int:
                     choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS)
                     + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS) + sorted(TREE_FP8_WORKLOADS)
                     + sorted(SELECT_WORKLOADS)
-                    + sorted(CONTIG_WORKLOADS) + sorted(DRAFT_STEP_WORKLOADS))
+                    + sorted(CONTIG_WORKLOADS) + sorted(DRAFT_STEP_WORKLOADS) + sorted(SGLANG_STEP_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--settle-ms", type=float, default=100.0,
@@ -906,6 +1082,9 @@ def main() -> int:
         return 0
     if args.workload in DRAFT_STEP_WORKLOADS:
         print(json.dumps(run_draft_step(args, dev)))
+        return 0
+    if args.workload in SGLANG_STEP_WORKLOADS:
+        print(json.dumps(run_sglang_step(args, dev)))
         return 0
 
     from flashmap_amd import _native, ops
@@ -969,14 +1148,10 @@ def main() -> int:
     ms, kernel_ms, timing = _time_call(call, args)
 
     ab = algorithmic_bytes(inp, kv_bytes=1 if fp8 else 2)
-    traffic = None
-    tfile = ROOT / "profiles" / f"attn_fwd_{args.workload.split('-', 1)[0]}_paged_b{batch}{'_fp8' if fp8 else ''}.traffic.json"
-    if tfile.exists():
-        rec = json.loads(tfile.read_text())
-        if rec.get("workload") == args.workload:
-            traffic = rec["traffic_bytes"]
+    traffic = traffic_record(f"attn_fwd_{args.workload.split('-', 1)[0]}_paged_b{batch}{'_fp8' if fp8 else ''}"
+                             ".traffic.json", args.workload)
     us = ms * 1e3
-    achieved = ab["total"] / (kernel_ms * 1e-3) / 1e9  # GB/s of the main kernel
+    achieved = ab["kernel"] / (kernel_ms * 1e-3) / 1e9  # GB/s of the main kernel on its own bytes
     result = {
         "metric": METRIC,
         "value": round(us, 2),
@@ -1010,7 +1185,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "bytes_per_launch": ab["total"],
+            "bytes_per_launch": ab["kernel"],
+            "call_bytes": ab["total"],
             "kernel_us": round(kernel_ms * 1e3, 2),
         },
         "mfma": mfma_record(args.workload, ab["flops"], kernel_ms, fp8),
