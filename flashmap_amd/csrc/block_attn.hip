@@ -1625,6 +1625,52 @@ __device__ __forceinline__ void prologue_global(u32x4_t (&x)[D / 32], const Attn
   }
 }
 
+// e4m3 query rows from the prologue's bf16 rows, as the query pass makes them (lane (n, g)
+// holds channels 32 t + 8 g .. + 7 of row n, the wavefront's 16 rows being one query head's
+// draft tokens): the head's scale max(amax, 1e-12) / 448 over the 16 rows, every value
+// divided by it (correctly rounded) and rounded to e4m3 (torch's (q / scale).to(e4m3)),
+// then moved across the row's four lanes into the fp8 MFMA operand layout: fragment f of
+// lane (n, g) holds channels 64 f + 16 g .. + 15. Word s of that fragment is chunk
+// c = 8 f + 2 g + s / 2 (8 channels), which the row-quad layout keeps in lane (n, c % 4),
+// register c / 4 = 2 f + g / 2, word s % 2. Returns the scale.
+template <int D>
+__device__ __forceinline__ float quantize_query_rows(const u32x4_t (&x)[D / 32], u32x4_t (&qf)[D / 64], int n,
+                                                     int g) {
+  constexpr int KT = D / 32;
+  float mx = 0.f;
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fmaxf(fabsf(bf16_lo(x[t][q])), fabsf(bf16_hi(x[t][q]))));
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = max_over_groups(mx);
+  const float scale = __fdiv_rn(fmaxf(mx, 1e-12f), 448.f);
+  u32x2_t q8[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[2 * q] = __fdiv_rn(bf16_lo(x[t][q]), scale);
+      v[2 * q + 1] = __fdiv_rn(bf16_hi(x[t][q]), scale);
+    }
+    q8[t] = u32x2_t{pack_e4m3x4(v[0], v[1], v[2], v[3]), pack_e4m3x4(v[4], v[5], v[6], v[7])};
+  }
+  const bool upper = (g >> 1) != 0;  // lanes of groups 2, 3 take register 2 f + 1
+#pragma unroll
+  for (int f = 0; f < D / 64; ++f) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int src = n + 16 * ((2 * g + (w >> 1)) & 3);
+      const int lo = __shfl((int)q8[2 * f][w & 1], src);
+      const int hi = __shfl((int)q8[2 * f + 1][w & 1], src);
+      qf[f][w] = (uint32_t)(upper ? hi : lo);
+    }
+  }
+  return scale;
+}
+
 // One workgroup = R replicas x (W consumer wavefronts + 1 producer wavefront).
 //
 // The producer issues every load of its replica's K/V stream (LDS-DMA into the ring, plus
@@ -1650,7 +1696,6 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   constexpr int RBUF = QTOK * D * 4;                  // DQ: a replica's rope buffer
   static_assert(S >= 3, "the wait schedule keeps one group between tiles");
   static_assert((S - 2) * G::NI + (S - 2) < 64, "vmcnt holds 6 bits");
-  static_assert(!(DQ && F8), "direct query rows are bf16");
   static_assert(SEQ >= 1, "LDS budget");
   __shared__ __attribute__((aligned(1024))) char smem_all[R * RBYTES];
   __shared__ i32x2_t seq_tab[SEQ + 1];
@@ -1846,8 +1891,15 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   // the unit starts.
   const int units = a.batch * a.ups;
   int qn_unit = -1;
-  u32x4_t qn[QF], qf[QF];
+  constexpr int QB = DQ ? D / 32 : QF;  // a lane's 16-byte registers of its query row as loaded
+  u32x4_t qn[QB], qf[QF];
   float rsn = 1.f, sl = a.scale_log2;
+  // F8 direct rows: the key descale of a unit's (sequence, KV head), loaded with its rows
+  auto kdesc = [&](int u) {
+    if (!F8 || a.kd == nullptr) return 1.f;
+    const int b = u / a.ups, h = (u - b * a.ups) / a.rgroups;
+    return *(g_float_t *)(a.kd + (int64_t)b * a.d_sb + (int64_t)h * a.d_sh);
+  };
   if (!DQ && ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < QF; ++t) qn[t] = *(g_u32x4_t *)(qsrc(cc.u) + 64 * t);
@@ -1870,6 +1922,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       }
       const QRowD x = direct_row(a, (lds_i32x2_t *)qmeta, cc.u, wave * 16 + n, g);
       direct_load_rows(a, x, qn);
+      if (F8) rsn = kdesc(cc.u);
       qn_ok = x.ok;
       qn_unit = cc.u;
       wait_vm<0>();
@@ -1885,32 +1938,41 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     if (i == 0 || cc.lt == 0) {  // a segment starts: its query rows, prologue applied
       bool ok = qn_ok;
       int tq = 0;
+      u32x4_t xr[QB];  // the rows as loaded (bf16)
+      float kd = rsn;
       if (qn_unit == cc.u) {
 #pragma unroll
-        for (int t = 0; t < QF; ++t) qf[t] = qn[t];
+        for (int t = 0; t < QB; ++t) xr[t] = qn[t];
         tq = direct_tq(a, cc.u, wave * 16 + n);
       } else {
         const QRowD x = direct_row(a, (lds_i32x2_t *)qmeta, cc.u, wave * 16 + n, g);
-        direct_load_rows(a, x, qf);
+        direct_load_rows(a, x, xr);
+        if (F8) kd = kdesc(cc.u);
         ok = x.ok;
         tq = x.tq;
       }
 #pragma unroll
-      for (int t = 0; t < QF; ++t) {
-        asm volatile("" : "+v"(qf[t]));
+      for (int t = 0; t < QB; ++t) {
+        asm volatile("" : "+v"(xr[t]));
         qn[t] = u32x4_t{0, 0, 0, 0};  // consumed: no registers held for it through the prologue
       }
       if (a.qn_w != nullptr) {
         if (rb_unit == cc.u) {
-          prologue_lds<D>(qf, w_tab, rbuf, tq, g, il, a.eps);
+          prologue_lds<D>(xr, w_tab, rbuf, tq, g, il, a.eps);
         } else {
           const int b = cc.u / a.ups;
-          prologue_global<D>(qf, a, w_tab, ((lds_i32_t *)rrow)[b * QTOK + tq], g, il);
+          prologue_global<D>(xr, a, w_tab, ((lds_i32_t *)rrow)[b * QTOK + tq], g, il);
         }
       }
 #pragma unroll
-      for (int t = 0; t < QF; ++t)
-        if (!ok) qf[t] = u32x4_t{0, 0, 0, 0};
+      for (int t = 0; t < QB; ++t)
+        if (!ok) xr[t] = u32x4_t{0, 0, 0, 0};
+      if constexpr (F8) {  // e4m3 rows per (sequence, query head), as the query pass makes them
+        sl = a.scale_log2 * (quantize_query_rows<D>(xr, qf, n, g) * kd);
+      } else {
+#pragma unroll
+        for (int t = 0; t < QF; ++t) qf[t] = xr[t];
+      }
       rb_unit = -1;
       qn_unit = -1;
       dma_unit = -1;
@@ -1918,6 +1980,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       if (cc.u + 1 < units && cc.lt + ntiles - i > cc.tiles) {  // the share reaches unit u + 1
         const QRowD x = direct_row(a, (lds_i32x2_t *)qmeta, cc.u + 1, wave * 16 + n, g);
         direct_load_rows(a, x, qn);
+        if (F8) rsn = kdesc(cc.u + 1);
         qn_ok = x.ok;
         qn_unit = cc.u + 1;
         if (a.qn_w != nullptr) dma_unit = cc.u + 1;
@@ -2373,19 +2436,24 @@ static AttnKernel pick_kernel(int w) {
 // prologue applied in the kernel (bf16, no verify tokens, q_len <= QTOK, the batch's
 // metadata fits the kernel's LDS, and a small call: at most one unit per two shares), else
 // packed by a query pass (pack_queries_kernel, or pack_queries_f8_kernel for e4m3 K/V).
-enum QMode { Q_DIRECT = 0, Q_PACKED = 1, Q_F8 = 2 };
+// Q_F8_DIRECT: e4m3 K/V with bf16 queries read from the caller's rows, the prologue and
+// the per-(sequence, head) quantization applied in the attention kernel (q_len 16).
+enum QMode { Q_DIRECT = 0, Q_PACKED = 1, Q_F8 = 2, Q_F8_DIRECT = 3 };
 
-template <int D>
+static bool is_f8(int qmode) { return qmode == Q_F8 || qmode == Q_F8_DIRECT; }
+static bool has_pass(int qmode) { return qmode == Q_PACKED || qmode == Q_F8; }
+
+template <int D, bool F8>
 static int dq_seq_cap(int w) {
   switch (w) {
-    case 1: return kernel_seq_cap<D, 1, false, true>();
-    case 2: return kernel_seq_cap<D, 2, false, true>();
-    case 3: return kernel_seq_cap<D, 3, false, true>();
-    case 4: return kernel_seq_cap<D, 4, false, true>();
-    case 5: return kernel_seq_cap<D, 5, false, true>();
-    case 6: return kernel_seq_cap<D, 6, false, true>();
-    case 7: return kernel_seq_cap<D, 7, false, true>();
-    default: return kernel_seq_cap<D, 8, false, true>();
+    case 1: return kernel_seq_cap<D, 1, F8, true>();
+    case 2: return kernel_seq_cap<D, 2, F8, true>();
+    case 3: return kernel_seq_cap<D, 3, F8, true>();
+    case 4: return kernel_seq_cap<D, 4, F8, true>();
+    case 5: return kernel_seq_cap<D, 5, F8, true>();
+    case 6: return kernel_seq_cap<D, 6, F8, true>();
+    case 7: return kernel_seq_cap<D, 7, F8, true>();
+    default: return kernel_seq_cap<D, 8, F8, true>();
   }
 }
 
@@ -2417,6 +2485,10 @@ static AttnKernel select_kernel(int layout, int d, int w, int qmode) {
   if (qmode == Q_F8) {
     if (d == 128) return layout == PAGED16 ? pick_kernel<PAGED16, 128, true, false>(w) : pick_kernel<PAGED, 128, true, false>(w);
     return layout == PAGED16 ? pick_kernel<PAGED16, 64, true, false>(w) : pick_kernel<PAGED, 64, true, false>(w);
+  }
+  if (qmode == Q_F8_DIRECT) {
+    if (d == 128) return layout == PAGED16 ? pick_kernel<PAGED16, 128, true, true>(w) : pick_kernel<PAGED, 128, true, true>(w);
+    return layout == PAGED16 ? pick_kernel<PAGED16, 64, true, true>(w) : pick_kernel<PAGED, 64, true, true>(w);
   }
   const bool dq = qmode == Q_DIRECT;
   if (d == 128) {
@@ -2516,7 +2588,7 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->rp = row_plan(hq / hkv, q_len);
   AttnKernel k = select_kernel(layout, d, sz->rp.nrb, qmode);
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
-  const int tile = qmode == Q_F8 ? TILE_F8 : TILE;
+  const int tile = is_f8(qmode) ? TILE_F8 : TILE;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + tile - 1) / tile);
   const Tuning &tu = tuning();
   const int min_tiles = tuned(tu.min_tiles, 8) > 0 ? tuned(tu.min_tiles, 8) : 1;
@@ -2540,7 +2612,7 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->plan_off = off;
   if (need_plan) off = align256(off + 2 * sizeof(int32_t) * ((size_t)batch + 1));
   sz->q_off = off;  // packed query rows (none for direct rows); fp8: a score scale per row
-  if (qmode != Q_DIRECT) off = align256(off + sizeof(uint16_t) * units * rows * d);
+  if (has_pass(qmode)) off = align256(off + sizeof(uint16_t) * units * rows * d);
   sz->rs_off = off;
   if (qmode == Q_F8) off = align256(off + sizeof(float) * units * rows);
   sz->lse_off = off;
@@ -2641,7 +2713,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     const bool inter = c.rope_ps == 2 && c.rope_sin == c.rope_cos + 1;
     const bool fast_rope = c.qn_w == nullptr || ((split || inter) && ((uintptr_t)c.rope_cos & 15) == 0 &&
                                                  c.rope_rs % 4 == 0 && ((uintptr_t)c.qn_w & 3) == 0);
-    const int cap = c.d == 128 ? dq_seq_cap<128>(rp.nrb) : dq_seq_cap<64>(rp.nrb);
+    const int cap = c.d == 128 ? dq_seq_cap<128, false>(rp.nrb) : dq_seq_cap<64, false>(rp.nrb);
     // Direct rows cost a prologue at every segment start, inside the workgroup's barrier
     // cycle (about 5000 shader cycles at 64 rows x D 128), which the cost cut of the line
     // absorbs (6 tiles per unit); the query pass costs a launch and one read + write of the
@@ -2653,6 +2725,23 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     const int64_t units = (int64_t)c.batch * c.hkv * rp.rgroups;
     const bool small = units <= sz.num_shares;
     if (fast_rope && c.batch <= cap && (force == 0 || (force < 0 && small))) qmode = Q_DIRECT;
+  }
+  // e4m3 K/V with bf16 queries of one 16-row block per query head: with
+  // FLASHMAP_QUERY_PASS=0 the attention kernel applies the prologue and quantizes each
+  // (sequence, head) itself, bit for bit as the pass does. Not the default: measured at
+  // batch 64 x 32/8 heads (C3's draw on an e4m3 cache), one box, the call takes 122.8 us
+  // at its best share cost (10 tiles; 141 us at 4) against 113.8 us with the pass: the
+  // quantization's 32 correctly rounded divisions per lane at every segment start sit in
+  // the workgroup's barrier cycle, and the kernel needs 168 VGPRs with a small spill.
+  if (a.f8 && !a.q_fp8 && vf == nullptr && c.q_len == QTOK) {
+    const RowPlan rp = row_plan(c.hq / c.hkv, c.q_len);
+    const bool split = c.rope_ps == 1 && ((uintptr_t)c.rope_sin & 15) == 0;
+    const bool inter = c.rope_ps == 2 && c.rope_sin == c.rope_cos + 1;
+    const bool fast_rope = c.qn_w == nullptr || ((split || inter) && ((uintptr_t)c.rope_cos & 15) == 0 &&
+                                                 c.rope_rs % 4 == 0 && ((uintptr_t)c.qn_w & 3) == 0);
+    const int cap = c.d == 128 ? dq_seq_cap<128, true>(rp.nrb) : dq_seq_cap<64, true>(rp.nrb);
+    const int force = tuned(tuning().query_pass, -1);
+    if (fast_rope && c.batch <= cap && force == 0) qmode = Q_F8_DIRECT;
   }
   // Small calls: attn_small_kernel with the caller's rows read directly (two launches),
   // unless the workspace was sized for the persistent kernel only (a static scratch).
@@ -2669,7 +2758,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
       small_tiles = 0;
     }
   }
-  if (small_tiles == 0 && qmode == Q_DIRECT) {
+  if (small_tiles == 0 && (qmode == Q_DIRECT || qmode == Q_F8_DIRECT)) {
     rc = sizing(layout, c.batch, c.q_len, c.hq, c.hkv, c.d, c.max_k, need_plan, &sz, vf != nullptr, qmode);
     if (rc != FM_OK) return rc;
   }
@@ -2709,7 +2798,9 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // the cut, and an extra cost only unbalances shares of equal units (batch 8 of
   // 32768-position sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
   // FLASHMAP_SHARE_COST overrides.
-  const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares ? (a.f8 ? 4 : qmode == Q_DIRECT ? 6 : 2) : 0;
+  const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares
+                          ? (qmode == Q_F8_DIRECT ? 10 : a.f8 ? 4 : qmode == Q_DIRECT ? 6 : 2)
+                          : 0;
   a.share_c = small_tiles > 0 ? 0 : tuned(tuning().share_cost, share_c);
   if (a.share_c < 0) a.share_c = 0;
   a.tail = vf != nullptr;
@@ -2721,7 +2812,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   a.part_o = (uint16_t *)(ws + sz.o_off);
   // A call without a plan makes its own: in the query pass's last workgroup when there is a
   // query pass (one launch fewer), else with attn_plan_kernel.
-  const bool pass = qmode != Q_DIRECT;
+  const bool pass = has_pass(qmode);
   if (a.seqlens != nullptr) {
     const int32_t *plan = c.plan;
     if (need_plan) {
@@ -2741,7 +2832,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   const int64_t qblocks = (units * sz.rp.nrb + 3) / 4 + (a.plan_out != nullptr ? 1 : 0);
   const VerifyArgs nov{};
-  if (qmode == Q_DIRECT) {
+  if (!pass) {
     // no query pass: the attention kernel reads the rows and applies the prologue
   } else if (a.f8 && c.d == 128) {
     pack_queries_f8_kernel<128><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a);
@@ -2756,7 +2847,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   } else {
     pack_queries_kernel<64, false><<<dim3((unsigned)qblocks), dim3(256), 0, c.stream>>>(a, nov);
   }
-  if (qmode != Q_DIRECT) FM_CHECK_HIP(hipGetLastError());
+  if (pass) FM_CHECK_HIP(hipGetLastError());
   AttnKernel k = small_tiles > 0 ? select_small(layout, c.d, sz.rp.nrb) : select_kernel(layout, c.d, sz.rp.nrb, qmode);
   const dim3 kblock(small_tiles > 0 ? 64 * (sz.rp.nrb + 1) : 64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb));
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
@@ -2836,6 +2927,11 @@ extern "C" size_t fm_attn_workspace_bytes(int32_t batch, int32_t max_seqlen_q, i
     rc = sizing(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, max_seqlen_k,
                 true, &sz, false, v >= 3 ? Q_F8 : Q_PACKED);
     if (rc == FM_OK && sz.bytes > bytes) bytes = sz.bytes;
+    if (rc == FM_OK && v >= 3) {  // e4m3 calls with direct rows (their kernel's grid may differ)
+      rc = sizing(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, max_seqlen_k, true, &sz,
+                  false, Q_F8_DIRECT);
+      if (rc == FM_OK && sz.bytes > bytes) bytes = sz.bytes;
+    }
     const int st = v < 3 ? small_tiles_for(layout, batch, max_seqlen_q, num_q_heads, num_kv_heads, head_dim,
                                            max_seqlen_k)
                          : 0;

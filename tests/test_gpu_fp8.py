@@ -227,3 +227,76 @@ def test_paged_fp8_own_plan_equals_step_plan(dev):
     step = o.block_attention_paged_fp8(q8, cache, cu, lens_d, bt.to(dev), k_rows, 3000, d ** -0.5,
                                        plan=o.attention_plan(lens_d))
     assert torch.equal(own, step)
+
+
+@pytest.mark.parametrize("descales", [False, True])
+@pytest.mark.parametrize("layout,d,hq,hkv", [("paged", 128, 32, 8), ("pool", 128, 32, 8), ("paged", 64, 8, 2),
+                                            ("pool", 64, 40, 8)])
+def test_fp8_direct_rows_equal_query_pass(dev, tuning, layout, d, hq, hkv, descales):
+    """e4m3 calls with bf16 queries: the attention kernel normalizes, rotates and quantizes
+    each (request, query head) of the caller's rows itself (direct rows), or the query pass
+    does: the same bits either way (the same prologue arithmetic, the same amax, the same
+    correctly rounded divisions), for ragged draft rows, a request without context and,
+    on vLLM's layout, key descales; both within the bar of the dequantized oracle."""
+    print(f"fp8 direct rows {layout} d={d} hq={hq} hkv={hkv} descales={descales}", flush=True)
+    g = gen(99 + descales + d)
+    page, k_rows = 16, 16
+    lens = torch.tensor([700, 33, 1, 260, 0, 1500])
+    bs = len(lens)
+    o = ops()
+    w = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(int(lens.max()) + k_rows + 1, d, 1e6)
+    pro_rows = torch.tensor([16, 9, 16, 3, 16, 16]) if layout == "paged" else torch.full((bs,), k_rows)
+    cu = torch.cat([torch.zeros(1, dtype=torch.int32), pro_rows.cumsum(0).to(torch.int32)])
+    pos = torch.cat([int(n) + torch.arange(int(r)) for n, r in zip(lens, pro_rows)])
+    n_tok = int(cu[-1])
+    q_pre = (torch.randn(n_tok, hq, d, generator=g) * 2).bfloat16()
+    pro = o.Prologue(w.to(dev), o.rope_from_table(table.to(dev)), pos.to(dev), 1e-6)
+    desc = (torch.rand(3, bs, hkv, generator=g) + 0.25) if descales else None
+    if layout == "paged":
+        bt, total = paged_layout(lens.tolist(), page, g)
+        cache = _e4m3((total, hkv, page, 2 * d), g)
+
+        def run():
+            return o.block_attention_paged_fp8(q_pre.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32),
+                                               bt.to(dev), k_rows, int(lens.max()), d ** -0.5, prologue=pro,
+                                               descales=None if desc is None else desc.to(dev))
+    else:
+        if descales:
+            pytest.skip("the pool call takes no descales (its pools are written with scale 1)")
+        pool = int(lens.sum()) + 11
+        perm = torch.randperm(pool, generator=g)
+        pt = torch.zeros(bs, int(lens.max()), dtype=torch.int32)
+        off = 0
+        for b in range(bs):
+            pt[b, :int(lens[b])] = perm[off:off + int(lens[b])].int()
+            off += int(lens[b])
+        kb, vb = _e4m3((pool, hkv, d), g), _e4m3((pool, hkv, d), g)
+
+        def run():
+            return o.block_attention_token_paged_fp8(q_pre.view(bs, k_rows, hq, d).to(dev), kb.to(dev), vb.to(dev),
+                                                     lens.to(dev, torch.int32), pt.to(dev), prologue=pro)
+    tuning("FLASHMAP_SHARE_COST", "4")  # one cut of the line for both
+    outs = {}
+    for mode in ("1", "0"):
+        tuning("FLASHMAP_QUERY_PASS", mode)
+        outs[mode] = run()
+    torch.cuda.synchronize()
+    assert torch.equal(outs["0"], outs["1"]), "direct rows differ from the query pass"
+    qn = ref.rms_norm_rope_vllm(q_pre, w, table, pos, 1e-6)
+    got = outs["0"].cpu().float().view(-1, hq, d)
+    if layout == "paged":
+        for b in range(bs):
+            s, e = int(cu[b]), int(cu[b + 1])
+            q8, qs = ref.quantize_query_per_head(qn[s:e][None])  # per (request, query head)
+            qdq = q8[0].float() * qs[0][None, :, None]
+            kv_desc = torch.ones(3, 1, hkv)
+            if desc is not None:
+                kv_desc[1:, 0] = desc[1:, b]
+            want = ref.block_attention_paged_vllm_fp8(qdq, cache, torch.tensor([0, e - s], dtype=torch.int32),
+                                                      lens[b:b + 1], bt[b:b + 1], d ** -0.5, kv_desc)
+            check_close(got[s:e], want)
+    else:
+        want = ref.block_attention_token_paged_fp8(qn.view(bs, k_rows, hq, d), kb, vb, lens, pt)
+        check_close(got.view(bs, k_rows, hq, d), want)
+
