@@ -109,7 +109,7 @@ def traffic_record(name: str, workload: str):
     return rec["traffic_bytes"]
 
 
-def mfma_record(workload: str, flops: float, kernel_ms: float, fp8: bool) -> dict:
+def mfma_record(workload: str, batch: int, flops: float, kernel_ms: float, fp8: bool) -> dict:
     """MFMA utilisation of the main kernel: from the rocprofv3 counters committed under
     profiles/ for this workload (SQ_VALU_MFMA_BUSY_CYCLES over the SIMD-cycles of the
     dispatch) when they were collected on the kernel sources being timed (else marked
@@ -117,8 +117,7 @@ def mfma_record(workload: str, flops: float, kernel_ms: float, fp8: bool) -> dic
     rec = {"tflops_algorithmic": round(flops / (kernel_ms * 1e-3) / 1e12, 1),
            "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
            "util_algorithmic": round(flops / (kernel_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
-    name = "attn_fwd_" + workload.split("-", 1)[0] + "_paged_b" + workload.rsplit("-b", 1)[1].split("-")[0] \
-        + ("_fp8" if fp8 else "") + ".mfma.json"
+    name = f"attn_fwd_{workload.split('-', 1)[0]}_paged_b{batch}{'_fp8' if fp8 else ''}.mfma.json"
     f = ROOT / "profiles" / name
     if f.exists():
         c = json.loads(f.read_text())
@@ -154,8 +153,13 @@ def algorithmic_bytes(inp, kv_bytes: int = 2) -> dict:
     rope = batch * k_rows * d * 4
     flops = 4 * k_rows * hq * d * sum_l
     total = kv + qo + table + meta + rope
-    # the main kernel's own share: everything but the output rows, which the combine writes
-    return dict(kv=kv, total=total, kernel=total - qo // 2, flops=flops, sum_l=sum_l)
+    # the main kernel's own share: everything but the output rows, which the combine writes;
+    # e4m3 calls: its queries are the pass's e4m3 rows and their scales (the pass applied the
+    # prologue: no rotary rows)
+    kernel = total - qo // 2
+    if kv_bytes == 1:
+        kernel = kv + batch * k_rows * hq * (d + 4) + table + meta
+    return dict(kv=kv, total=total, kernel=kernel, flops=flops, sum_l=sum_l)
 
 
 def cpu_paged_cache(inp, table) -> torch.Tensor:
@@ -1189,7 +1193,7 @@ def main() -> int:
             "call_bytes": ab["total"],
             "kernel_us": round(kernel_ms * 1e3, 2),
         },
-        "mfma": mfma_record(args.workload, ab["flops"], kernel_ms, fp8),
+        "mfma": mfma_record(args.workload, batch, ab["flops"], kernel_ms, fp8),
         **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:

@@ -47,6 +47,9 @@ PAGE = 16
 CASES = {
     "gelu_full_vocab": dict(mlp_type="gelu"),
     "swiglu_state_vocab": dict(mlp_type="swiglu", state_vocab_size=200),
+    # vLLM's d2t: a draft vocabulary restricting the logits while the state stays on the
+    # whole vocabulary (its jump head then spans every token)
+    "gelu_hot_ids": dict(mlp_type="gelu"),
 }
 BASE = dict(target_hidden_size=128, vocab_size=512, target_layer_ids=[0, 1], block_size=16, hidden_size=256,
             num_hidden_layers=2, num_attention_heads=2, intermediate_size=512, cond_dim=32, time_embed_dim=32,
@@ -196,12 +199,15 @@ def _oracle_weights(model, embed, lm_head, hot, steps, max_positions):
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_draft_step_matches_the_oracle(dev, name, steps):
     print(f"draft step {name}, {steps} jump(s)", flush=True)
-    model = _model(CASES[name], dev, 11)
+    over = dict(CASES[name])
+    model = _model(over, dev, 11)
     cfg = model.config
     g = gen(5)
     embed = torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=g).bfloat16().to(dev)
     lm_head = (torch.randn(cfg.vocab_size, cfg.target_hidden_size, generator=g) / 8).bfloat16().to(dev)
     hot = torch.arange(0, 2 * cfg.state_vocab_size, 2).to(dev) if cfg.state_vocab_size else None
+    if name == "gelu_hot_ids":
+        hot = torch.arange(3, cfg.vocab_size, 3).to(dev)
     step = DraftStep(model, embed, lm_head, max_model_len=512, hot_ids=hot, num_steps=steps)
     lens = torch.tensor([37, 100, 0, 64])  # context positions before each anchor
     batch, k = len(lens), cfg.block_size
