@@ -104,6 +104,8 @@ SIGNATURES: dict[str, tuple] = {
     "fm_seeded_normal": (c_int, [P, P, I32, P, I32, I64, I64, F32, P, I64, P]),
     "fm_adaln_residual": (c_int, [P, I64, P, I64, P, I32, P, P, P, I64, P, I64, I64, I32, F32, P]),
     "fm_noise_rows": (c_int, [P, I64, I32, I64, P, F32, F32, P, I64, P, P]),
+    "fm_state_embed_rows": (c_int, [P, I64, I64, I64, F32, I32, P, I64, P]),
+    "fm_state_update": (c_int, [P, I64, I64, I64, P, I64, c_double, c_double, P]),
     "fm_profile_enable": (c_int, [c_int]),
     "fm_clock_probe": (c_int, [P, ctypes.c_uint64, P]),
     "fm_profile_read": (c_int, [ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]),

@@ -155,6 +155,144 @@ __global__ __launch_bounds__(256) void noise_rows_kernel(const float *__restrict
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// The several-jump draft's state over the vocabulary (flashmap/vllm/model.py:944-956,
+// 1031-1036): softmaxes over rows of up to ~10^5 fp32 values, one workgroup per row.
+// The row is read twice: once for its statistics (max and sum of exponentials, online
+// per thread, merged over the workgroup), once for the outputs (each thread re-reads the
+// 16-byte chunks it read the first time; a row is small enough to be served from the
+// cache the second time). Exponentials are expf; the division and the update use torch's
+// rounding points.
+constexpr int STATE_THREADS = 256;
+
+struct RowStats {
+  float m, s;  // max and sum of exp(x - m)
+};
+
+__device__ __forceinline__ RowStats merge_stats(RowStats a, RowStats b) {
+  const float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return RowStats{m, 0.f};
+  const float sa = a.m == -INFINITY ? 0.f : __fmul_rn(a.s, expf(__fsub_rn(a.m, m)));
+  const float sb = b.m == -INFINITY ? 0.f : __fmul_rn(b.s, expf(__fsub_rn(b.m, m)));
+  return RowStats{m, __fadd_rn(sa, sb)};
+}
+
+__device__ __forceinline__ void add_chunk(RowStats &st, const float (&x)[4]) {
+  const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  if (mx == -INFINITY) return;  // nothing to add (and no exp(-inf - -inf))
+  if (mx > st.m) {
+    st.s = st.m == -INFINITY ? 0.f : __fmul_rn(st.s, expf(__fsub_rn(st.m, mx)));
+    st.m = mx;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) st.s = __fadd_rn(st.s, expf(__fsub_rn(x[q], st.m)));
+}
+
+// The workgroup's statistics from each thread's.
+__device__ __forceinline__ RowStats block_stats(RowStats st) {
+  __shared__ RowStats part[STATE_THREADS / 64];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const RowStats other{__shfl_xor(st.m, o, 64), __shfl_xor(st.s, o, 64)};
+    st = merge_stats(st, other);
+  }
+  if ((threadIdx.x & 63) == 0) part[wave_id()] = st;
+  __syncthreads();
+  RowStats r = part[0];
+#pragma unroll
+  for (int w = 1; w < STATE_THREADS / 64; ++w) r = merge_stats(r, part[w]);
+  return r;
+}
+
+// POST: rows r < rows of out get bf16(softmax(evidence * state[r])) and rows rows + r
+// bf16(state[r]); otherwise out holds the state rows only (one read of the row).
+template <bool POST>
+__global__ __launch_bounds__(STATE_THREADS) void state_embed_rows_kernel(const float *__restrict__ state,
+                                                                         int64_t vocab, int64_t ss, float evidence,
+                                                                         uint16_t *__restrict__ out, int64_t os,
+                                                                         int64_t rows) {
+  const int64_t row = blockIdx.x;
+  const float *x = state + row * ss;
+  const int64_t chunks = vocab >> 2;
+  if constexpr (!POST) {
+    uint16_t *raw = out + row * os;
+#pragma unroll 4
+    for (int64_t c = threadIdx.x; c < chunks; c += STATE_THREADS) {
+      const f32x4_t v = *reinterpret_cast<const f32x4_t *>(x + 4 * c);
+      *reinterpret_cast<u32x2_t *>(raw + 4 * c) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+    for (int64_t i = 4 * chunks + threadIdx.x; i < vocab; i += STATE_THREADS)
+      raw[i] = (uint16_t)(pack_bf16x2(x[i], 0.f) & 0xffffu);
+    return;
+  }
+  RowStats st{-INFINITY, 0.f};
+#pragma unroll 4
+  for (int64_t c = threadIdx.x; c < chunks; c += STATE_THREADS) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t *>(x + 4 * c);
+    const float e[4] = {__fmul_rn(v[0], evidence), __fmul_rn(v[1], evidence), __fmul_rn(v[2], evidence),
+                        __fmul_rn(v[3], evidence)};
+    add_chunk(st, e);
+  }
+  for (int64_t i = 4 * chunks + threadIdx.x; i < vocab; i += STATE_THREADS) {  // the tail (vocab % 4)
+    const float e[4] = {__fmul_rn(x[i], evidence), -INFINITY, -INFINITY, -INFINITY};
+    add_chunk(st, e);
+  }
+  const RowStats t = block_stats(st);
+  uint16_t *post = out + row * os, *raw = out + (rows + row) * os;
+#pragma unroll 4
+  for (int64_t c = threadIdx.x; c < chunks; c += STATE_THREADS) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t *>(x + 4 * c);
+    float p[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) p[q] = __fdiv_rn(expf(__fsub_rn(__fmul_rn(v[q], evidence), t.m)), t.s);
+    *reinterpret_cast<u32x2_t *>(post + 4 * c) = u32x2_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    *reinterpret_cast<u32x2_t *>(raw + 4 * c) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+  for (int64_t i = 4 * chunks + threadIdx.x; i < vocab; i += STATE_THREADS) {
+    const float p = __fdiv_rn(expf(__fsub_rn(__fmul_rn(x[i], evidence), t.m)), t.s);
+    post[i] = (uint16_t)(pack_bf16x2(p, 0.f) & 0xffffu);
+    raw[i] = (uint16_t)(pack_bf16x2(x[i], 0.f) & 0xffffu);
+  }
+}
+
+// state[r] = (c_keep * state[r] + c_new * softmax(logits[r])) / c_div in place, logits bf16.
+__global__ __launch_bounds__(STATE_THREADS) void state_update_kernel(float *__restrict__ state, int64_t vocab,
+                                                                     int64_t ss, const uint16_t *__restrict__ logits,
+                                                                     int64_t ls, float c_keep, float c_new,
+                                                                     float c_div) {
+  const int64_t row = blockIdx.x;
+  float *x = state + row * ss;
+  const uint16_t *lg = logits + row * ls;
+  const int64_t chunks = vocab >> 2;
+  RowStats st{-INFINITY, 0.f};
+#pragma unroll 4
+  for (int64_t c = threadIdx.x; c < chunks; c += STATE_THREADS) {
+    const u32x2_t w = *reinterpret_cast<const u32x2_t *>(lg + 4 * c);
+    const float e[4] = {bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+    add_chunk(st, e);
+  }
+  for (int64_t i = 4 * chunks + threadIdx.x; i < vocab; i += STATE_THREADS) {
+    const float e[4] = {__uint_as_float((uint32_t)lg[i] << 16), -INFINITY, -INFINITY, -INFINITY};
+    add_chunk(st, e);
+  }
+  const RowStats t = block_stats(st);
+  auto upd = [&](float s, float l) {
+    const float d = __fdiv_rn(expf(__fsub_rn(l, t.m)), t.s);
+    return __fdiv_rn(__fadd_rn(__fmul_rn(c_keep, s), __fmul_rn(c_new, d)), c_div);
+  };
+#pragma unroll 4
+  for (int64_t c = threadIdx.x; c < chunks; c += STATE_THREADS) {
+    const u32x2_t w = *reinterpret_cast<const u32x2_t *>(lg + 4 * c);
+    f32x4_t v = *reinterpret_cast<const f32x4_t *>(x + 4 * c);
+    v[0] = upd(v[0], bf16_lo(w[0]));
+    v[1] = upd(v[1], bf16_hi(w[0]));
+    v[2] = upd(v[2], bf16_lo(w[1]));
+    v[3] = upd(v[3], bf16_hi(w[1]));
+    *reinterpret_cast<f32x4_t *>(x + 4 * c) = v;
+  }
+  for (int64_t i = 4 * chunks + threadIdx.x; i < vocab; i += STATE_THREADS)
+    x[i] = upd(x[i], __uint_as_float((uint32_t)lg[i] << 16));
+}
+
 }  // namespace fm
 
 extern "C" int fm_adaln_residual(const void *x, int64_t x_stride, const void *y, int64_t y_stride,
@@ -227,6 +365,49 @@ extern "C" int fm_noise_rows(const float *z, int64_t rows, int32_t hidden, int64
     noise_rows_kernel<16><<<grid, block, 0, s>>>(z, rows, hidden, z_stride, eigvals, eps, gain, zo, z_bf16_stride, so);
   else
     noise_rows_kernel<64><<<grid, block, 0, s>>>(z, rows, hidden, z_stride, eigvals, eps, gain, zo, z_bf16_stride, so);
+  FM_CHECK_HIP(hipGetLastError());
+  return FM_OK;
+}
+
+extern "C" int fm_state_embed_rows(const float *state, int64_t rows, int64_t vocab, int64_t state_stride,
+                                   float evidence, int32_t posterior, void *out, int64_t out_stride, void *stream) {
+  using namespace fm;
+  FM_REQUIRE(rows >= 0 && vocab > 0, "bad sizes: rows=%lld vocab=%lld", (long long)rows, (long long)vocab);
+  if (rows == 0) return FM_OK;
+  FM_REQUIRE(state && out, "NULL tensor pointer");
+  FM_REQUIRE(rows < (1ll << 31), "too many rows");
+  FM_REQUIRE(aligned16(state) && state_stride % 4 == 0 && state_stride >= vocab,
+             "state must be 16-byte aligned with a row stride that is a multiple of 4 covering a row");
+  FM_REQUIRE(((uintptr_t)out & 7) == 0 && out_stride % 4 == 0 && out_stride >= vocab,
+             "out must be 8-byte aligned with a row stride that is a multiple of 4 covering a row");
+  const dim3 grid((unsigned)rows), block(STATE_THREADS);
+  if (posterior)
+    state_embed_rows_kernel<true><<<grid, block, 0, (hipStream_t)stream>>>(state, vocab, state_stride, evidence,
+                                                                           (uint16_t *)out, out_stride, rows);
+  else
+    state_embed_rows_kernel<false><<<grid, block, 0, (hipStream_t)stream>>>(state, vocab, state_stride, evidence,
+                                                                            (uint16_t *)out, out_stride, rows);
+  FM_CHECK_HIP(hipGetLastError());
+  return FM_OK;
+}
+
+extern "C" int fm_state_update(float *state, int64_t rows, int64_t vocab, int64_t state_stride, const void *logits,
+                               int64_t logits_stride, double start, double end, void *stream) {
+  using namespace fm;
+  FM_REQUIRE(rows >= 0 && vocab > 0, "bad sizes: rows=%lld vocab=%lld", (long long)rows, (long long)vocab);
+  if (rows == 0) return FM_OK;
+  FM_REQUIRE(state && logits, "NULL tensor pointer");
+  FM_REQUIRE(rows < (1ll << 31), "too many rows");
+  FM_REQUIRE(start < 1.0 && end >= start, "jump times must satisfy start <= end, start < 1 (got %g, %g)", start, end);
+  FM_REQUIRE(aligned16(state) && state_stride % 4 == 0 && state_stride >= vocab,
+             "state must be 16-byte aligned with a row stride that is a multiple of 4 covering a row");
+  FM_REQUIRE(((uintptr_t)logits & 7) == 0 && logits_stride % 4 == 0 && logits_stride >= vocab,
+             "logits must be 8-byte aligned with a row stride that is a multiple of 4 covering a row");
+  // The scalars as torch takes Python floats into a float32 op: computed in double, then
+  // rounded to float.
+  const float c_keep = (float)(1.0 - end), c_new = (float)(end - start), c_div = (float)(1.0 - start);
+  state_update_kernel<<<dim3((unsigned)rows), dim3(STATE_THREADS), 0, (hipStream_t)stream>>>(
+      state, vocab, state_stride, (const uint16_t *)logits, logits_stride, c_keep, c_new, c_div);
   FM_CHECK_HIP(hipGetLastError());
   return FM_OK;
 }

@@ -23,7 +23,9 @@ and the head the state moves with. A call runs the step of flashmap/vllm/model.p
    ``fm_adaln_residual`` (fused with the next layer's norm, or the final one);
 4. the folded head GEMM and, for greedy drafts, ``fm_argmax_rows``.
 
-GEMMs are hipBLASLt through torch; the state's softmaxes and update are torch ops.
+GEMMs are hipBLASLt through torch. With several jumps, the state's softmaxes run as two
+row kernels (``ops.state_embed_rows``: posterior and state as the embedding GEMM's bf16
+operand; ``ops.state_update``: the jump head's softmax and the update, in place).
 Inputs are explicit (what vLLM's forward context supplies): anchors and their positions
 and slots, the noise, the caches, the block table. bf16 only.
 """
@@ -38,6 +40,21 @@ from .drafter import FlashMapDraftModel, jump_times
 from .fold import fold_head, fold_noise
 
 __all__ = ["DraftStep"]
+
+
+def _split_k(a: torch.Tensor, w: torch.Tensor, splits: int = 4) -> torch.Tensor:
+    """``a @ w`` for a long reduction (the vocabulary) and few rows: ``splits`` slices of
+    the reduction as one batched GEMM with float32 partials, summed, rounded once to bf16
+    (hipBLASLt's single GEMM covers a quarter of the CUs at 1024 x 4096 outputs:
+    measured 2.00 -> 1.06 ms at 1024 x 151936 x 4096). Falls back to ``a @ w`` when the
+    reduction does not split evenly."""
+    rows, k = a.shape
+    if k % splits or a.stride(-1) != 1 or not w.is_contiguous():
+        return a @ w
+    part = k // splits
+    a3 = a.view(rows, splits, part).transpose(0, 1)  # (splits, rows, part), rows keep their stride
+    w3 = w.view(splits, part, w.shape[1])             # contiguous slices: no transposed operand
+    return torch.bmm(a3, w3, out_dtype=torch.float32).sum(0).to(w.dtype)
 
 
 def _rope_table(positions: int, head_dim: int, theta: float, device) -> torch.Tensor:
@@ -86,7 +103,8 @@ class DraftStep:
         state_embed = embed_tokens[hot_ids] if state_vocab else embed_tokens
         vocab = state_embed.shape[0]
         uniform = torch.full((1, vocab), 1.0 / vocab, device=state_embed.device, dtype=state_embed.dtype)
-        self.first_hidden = model.x_embed(model.state_norm(uniform @ state_embed))[0].contiguous()
+        self.uniform_emb = uniform @ state_embed  # the embedding of a uniform posterior (1, H)
+        self.first_hidden = model.x_embed(model.state_norm(self.uniform_emb))[0].contiguous()
         self.noise_embed, self.noise_eigvals = fold_noise(state_embed, model.noise_norm.weight, model.x_embed.weight)
         self.noise_eps = model.noise_norm.eps
         self.embed_weight = embed_tokens
@@ -181,7 +199,11 @@ class DraftStep:
             hidden, h = ops.adaln_residual(self.first_hidden, noise, row_scale, self._first_norm(0), eps,
                                            gate_per_row=True)
             return self._dit(hidden, h, 0, attend)
-        state = z
+        # The state is updated in place between the jumps: a copy of the caller's noise,
+        # in rows padded to a multiple of 4 values (the row kernels' 16-byte chunks).
+        vocab = z.shape[1]
+        state = torch.empty(z.shape[0], -(-vocab // 4) * 4, dtype=torch.float32, device=z.device)[:, :vocab]
+        state.copy_(z)
         h = None
         for step, (start, _, end) in enumerate(self.jumps):
             hidden = self._embed_state(state, step)
@@ -189,8 +211,7 @@ class DraftStep:
             h = ops.adaln_residual(hidden, None, None, self._first_norm(step), eps)[1]
             h = self._dit(hidden, h, step, attend)
             if step + 1 < self.num_steps:
-                delta = F.linear(h, *self.jump_head).float().softmax(dim=-1)
-                state = ((1.0 - end) * state + (end - start) * delta) / (1.0 - start)
+                ops.state_update(state, F.linear(h, *self.jump_head), start, end)
         return h
 
     def _first_norm(self, step: int):
@@ -206,11 +227,15 @@ class DraftStep:
         model, weight = self.model, self.state_weight
         start = self.time_grid[step]
         evidence = start / max(1.0 - start, 1e-3) ** 2
-        posterior = (state * evidence).softmax(dim=-1)
-        both = torch.cat([posterior, state]).to(weight.dtype) @ weight
-        posterior_emb, state_emb = both.split(state.shape[0])
+        if start == 0.0:  # evidence 0: the posterior is uniform, its embedding one row
+            state_emb = _split_k(ops.state_embed_rows(state, 0.0, posterior=False), weight)
+            posterior = model.state_norm(self.uniform_emb)  # (1, H), every row's
+        else:
+            both = ops.state_embed_rows(state, evidence) @ weight
+            posterior_emb, state_emb = both.split(state.shape[0])
+            posterior = model.state_norm(posterior_emb)
         embedded = (self.noise_gains[step] * model.noise_norm(state_emb)).to(weight.dtype)
-        return model.x_embed(model.state_norm(posterior_emb) + embedded)
+        return model.x_embed(posterior + embedded)
 
     def _dit(self, hidden: torch.Tensor, h: torch.Tensor, step: int, attend) -> torch.Tensor:
         """The DiT layers of jump ``step`` from the residual stream ``hidden`` and its

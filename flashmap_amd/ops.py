@@ -1232,5 +1232,55 @@ def noise_rows(z: torch.Tensor, eigvals: torch.Tensor, eps: float, gain: float,
     return z_bf16, scale
 
 
+def _state_rows(state: torch.Tensor) -> None:
+    if state.dtype != torch.float32 or state.dim() != 2 or state.stride(-1) != 1:
+        raise ValueError("the state must be float32 (rows, vocab) with unit column stride")
+    if state.stride(0) % 4 or state.data_ptr() % 16:
+        raise ValueError("the state's row stride must be a multiple of 4 and its data 16-byte aligned")
+
+
+def state_embed_rows(state: torch.Tensor, evidence: float, out: torch.Tensor | None = None,
+                     posterior: bool = True) -> torch.Tensor:
+    """``torch.cat([softmax(evidence * state), state]).to(bf16)`` for the several-jump
+    draft's state ``(rows, vocab)`` float32 (flashmap/vllm/model.py:944-956): one kernel
+    reading each row twice, ``(2 rows, vocab)`` bf16, the operand of the state
+    embedding's GEMM. ``posterior=False``: the state rows alone ``(rows, vocab)`` (one
+    read), for a jump whose posterior is uniform."""
+    _check_cuda(state, out)
+    _state_rows(state)
+    rows, vocab = state.shape
+    n = 2 * rows if posterior else rows
+    if out is None:  # rows padded to a multiple of 4 values
+        out = torch.empty(n, -(-vocab // 4) * 4, dtype=torch.bfloat16, device=state.device)[:, :vocab]
+    elif (out.dtype != torch.bfloat16 or tuple(out.shape) != (n, vocab) or out.stride(-1) != 1
+          or out.stride(0) % 4 or out.data_ptr() % 8):
+        raise ValueError(f"out must be bf16 ({n}, {vocab}) with unit column stride, a row stride of a "
+                         f"multiple of 4 and 8-byte alignment; got {out.dtype} {tuple(out.shape)} {out.stride()}")
+    if rows:
+        call("fm_state_embed_rows", state.data_ptr(), rows, vocab, state.stride(0), float(evidence),
+             int(posterior), out.data_ptr(), out.stride(0), _stream(state))
+    return out
+
+
+def state_update(state: torch.Tensor, logits: torch.Tensor, start: float, end: float) -> torch.Tensor:
+    """The state update between two jumps, in place (flashmap/vllm/model.py:1031-1036):
+    ``state = ((1 - end) state + (end - start) softmax(logits)) / (1 - start)`` with
+    ``logits (rows, vocab)`` bf16, in float32 with torch's rounding points."""
+    _check_cuda(state, logits)
+    _state_rows(state)
+    rows, vocab = state.shape
+    if logits.dtype != torch.bfloat16 or tuple(logits.shape) != (rows, vocab):
+        raise ValueError(f"logits must be bf16 ({rows}, {vocab}); got {logits.dtype} {tuple(logits.shape)}")
+    if logits.stride(-1) != 1 or logits.stride(0) % 4 or logits.data_ptr() % 8:  # into rows of 4k values
+        padded = torch.empty(rows, -(-vocab // 4) * 4, dtype=torch.bfloat16, device=logits.device)[:, :vocab]
+        logits = padded.copy_(logits)
+    if not (start < 1.0 and end >= start):
+        raise ValueError(f"jump times must satisfy start <= end and start < 1, got {start}, {end}")
+    if rows:
+        call("fm_state_update", state.data_ptr(), rows, vocab, state.stride(0), logits.data_ptr(),
+             logits.stride(0), float(start), float(end), _stream(state))
+    return state
+
+
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)

@@ -442,6 +442,27 @@ int fm_noise_rows(const float *z, int64_t rows, int32_t hidden, int64_t z_stride
                   const float *eigvals, float eps, float gain, void *z_bf16,
                   int64_t z_bf16_stride, void *scale, void *stream);
 
+/* The several-jump draft's state over the vocabulary (flashmap/vllm/model.py:944-956,
+ * `_embed_state`): for state (rows, vocab) fp32 with a row stride and posterior nonzero,
+ * out rows r < rows get bf16(softmax(evidence * state[r])) and rows rows + r get
+ * bf16(state[r]) -- the operand of the one GEMM through the state vocabulary's embedding
+ * (torch.cat([posterior, state]).to(bf16)); out is (2 rows, vocab) bf16 with a row
+ * stride. With posterior zero (a jump starting at time 0, whose posterior is uniform),
+ * out is (rows, vocab): the state rows only. Strides multiples of 4; state 16-byte
+ * aligned, out 8-byte aligned.
+ */
+int fm_state_embed_rows(const float *state, int64_t rows, int64_t vocab, int64_t state_stride,
+                        float evidence, int32_t posterior, void *out, int64_t out_stride, void *stream);
+
+/* The state update between two jumps (flashmap/vllm/model.py:1031-1036): with logits
+ * (rows, vocab) bf16 (the jump head's output) and the jump's times start <= end, start < 1:
+ * state = ((1 - end) * state + (end - start) * softmax(logits)) / (1 - start) in place,
+ * in float32 with torch's rounding points (the scalars rounded from double to float).
+ * Strides multiples of 4; state 16-byte aligned, logits 8-byte aligned.
+ */
+int fm_state_update(float *state, int64_t rows, int64_t vocab, int64_t state_stride, const void *logits,
+                    int64_t logits_stride, double start, double end, void *stream);
+
 /* ---------------------------------------------------------------------------------
  * Measurement hook. No reference counterpart: it lets a benchmark time the main
  * split-KV attention kernel alone with HIP events on the stream it runs on, without

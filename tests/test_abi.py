@@ -114,6 +114,15 @@ def test_residual_stream_argument_errors(lib):
     assert rc == n.FM_ERR_UNSUPPORTED and "hidden 30" in _err(lib)
     rc = lib.fm_noise_rows(x, 4, 32, 30, x, f, f, x, 32, x, None)
     assert rc == n.FM_ERR_INVALID and "row strides" in _err(lib)
+    rc = lib.fm_state_embed_rows(x, 4, 30, 30, f, 1, x, 32, None)
+    assert rc == n.FM_ERR_INVALID and "state must be 16-byte aligned" in _err(lib)
+    rc = lib.fm_state_embed_rows(x, 4, 32, 32, f, 1, ctypes.c_void_p(20), 32, None)
+    assert rc == n.FM_ERR_INVALID and "out must be 8-byte aligned" in _err(lib)
+    assert lib.fm_state_embed_rows(None, 0, 32, 32, f, 1, None, 32, None) == n.FM_OK
+    rc = lib.fm_state_update(x, 4, 32, 32, x, 32, 1.0, 1.0, None)
+    assert rc == n.FM_ERR_INVALID and "jump times" in _err(lib)
+    rc = lib.fm_state_update(x, 4, 32, 32, x, 30, 0.0, 0.5, None)
+    assert rc == n.FM_ERR_INVALID and "logits must be 8-byte aligned" in _err(lib)
 
 
 def test_plan_and_workspace_sizes_without_device(lib):
