@@ -919,12 +919,14 @@ __device__ __forceinline__ void compute_tile(const AttnArgs &a, const char *stag
 #pragma unroll
   for (int k = 3; k + 1 < 4 * NH; k += 2) mx = max3f(mx, s[k / 4][k % 4], s[(k + 1) / 4][(k + 1) % 4]);
   mx = max3f(mx, s[NH - 1][3], s[NH - 1][3]);  // 4 NH - 3 values after the first three: an odd count
-  mx = max_over_groups(mx) * sl;
+  mx *= sl;  // this lane group's max (sl > 0, so scaling and max commute)
   // Lazy rescale: the reference max m moves only when a row's tile max exceeds it by
   // more than 8 (log2 units), so P <= 2^8 in between and O^T/l are rescaled rarely. This
-  // is exact: O and l share the reference, and the output is O / l.
+  // is exact: O and l share the reference, and the output is O / l. A row's max exceeds
+  // m + 8 exactly when one of its four lane groups' does (the row's lanes hold the same
+  // m), so the row max across the groups is formed only when m moves.
   if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
-    const float mnew = fmaxf(m, mx);
+    const float mnew = fmaxf(m, max_over_groups(mx));
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 0 on the first tile (m = -inf)
     m = mnew;
     l *= alpha;
