@@ -76,6 +76,12 @@ constexpr int MAX_RUNS = 8;   // paged: runs of KV heads over several caches
 // wavefronts (3 per SIMD, so up to 168 VGPRs each).
 __host__ __device__ constexpr int replicas(int w) { return 2 * (w + 1) <= 12 ? 2 : 1; }
 
+// bf16 one-replica workgroups (W >= 6 row blocks) stream 64-position line tiles, each ring
+// slot holding two 32-position stages: the barrier cycle costs about the same at every
+// tile size (the producer's page ids and hand-off, the consumers' bookkeeping), so one
+// replica moves twice the bytes per cycle (two replicas already move two tiles).
+__host__ __device__ constexpr bool double_tiles(int w, bool f8) { return !f8 && replicas(w) == 1; }
+
 enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 
 // K/V geometry of the units.
@@ -127,6 +133,7 @@ struct AttnArgs {
   // q_fp8: the caller's queries are e4m3 already (else bf16, quantized per (sequence,
   // query head) with scale amax / 448).
   int32_t f8, q_fp8;
+  int32_t t64;  // the line's tiles are 64 positions (e4m3, and bf16 one-replica workgroups)
   float *q_rs;
   const float *qd, *kd, *vd;
   int64_t d_sb, d_sh;
@@ -1452,7 +1459,8 @@ constexpr int QTOK = 16;
 template <int D, int W, bool F8, bool DQ>
 __host__ __device__ constexpr int kernel_seq_cap() {
   using G = Geo<D, F8>;
-  constexpr int fixed = replicas(W) * (G::SMEM + OutSlot<D, W>::BYTES) + (DQ ? replicas(W) * QTOK * D * 4 + D * 4 : 0);
+  constexpr int ring = G::SMEM * (double_tiles(W, F8) ? 2 : 1);
+  constexpr int fixed = replicas(W) * (ring + OutSlot<D, W>::BYTES) + (DQ ? replicas(W) * QTOK * D * 4 + D * 4 : 0);
   constexpr int per = 8 + (DQ ? 8 + 4 * QTOK : 0);  // (prefix, length); (first token, rows) and rope rows
   constexpr int cap = (163840 - fixed - 1024) / per - 1;
   return cap < SEQ_LDS ? cap : SEQ_LDS;
@@ -1693,11 +1701,16 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   constexpr bool IDS = LAYOUT != CONTIG;  // page ids join the load stream
   constexpr int R = replicas(W);
   constexpr int S = G::NS;
-  constexpr int RBYTES = G::SMEM + O::BYTES;  // per replica: the ring, then the out slot
+  constexpr bool DBL = double_tiles(W, F8);      // two 32-position stages per line tile
+  constexpr int SUB = DBL ? 2 : 1;
+  constexpr int TL = SUB * G::T;                 // positions per line tile
+  constexpr int SLOT = SUB * G::STAGE;           // bytes per ring slot
+  constexpr int GN = SUB * G::NI, GI = SUB;      // loads and page-id loads per line tile
+  constexpr int RBYTES = S * SLOT + O::BYTES;    // per replica: the ring, then the out slot
   constexpr int SEQ = kernel_seq_cap<D, W, F8, DQ>();  // sequences whose metadata is staged in LDS
   constexpr int RBUF = QTOK * D * 4;                  // DQ: a replica's rope buffer
   static_assert(S >= 3, "the wait schedule keeps one group between tiles");
-  static_assert((S - 2) * G::NI + (S - 2) < 64, "vmcnt holds 6 bits");
+  static_assert((S - 2) * GN + (S - 2) * GI < 64, "vmcnt holds 6 bits");
   static_assert(SEQ >= 1, "LDS budget");
   __shared__ __attribute__((aligned(1024))) char smem_all[R * RBYTES];
   __shared__ i32x2_t seq_tab[SEQ + 1];
@@ -1767,7 +1780,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   __builtin_assume(wave >= 0 && wave <= W && rep >= 0 && rep < R);
   const int n = lane & 15, g = lane >> 4;
   char *const smem = smem_all + rep * RBYTES;
-  char *const out = smem + G::SMEM;
+  char *const out = smem + S * SLOT;
   const int share = (int)blockIdx.x * R + rep;
   int64_t F[R + 1];  // first tiles of the workgroup's shares and the next one
   share_first_tiles(a, sm, (int64_t)blockIdx.x * R, F);
@@ -1784,7 +1797,7 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   }
   Cursor cc = Cursor{0, 0, 0, 0, 0, 0, 0, 0};  // tile being computed (i)
   if (ntiles > 0) cc = cursor_at(a, sm, T0);
-  auto stage = [&](int t) { return smem + (t % S) * G::STAGE; };
+  auto stage = [&](int t) { return smem + (t % S) * SLOT; };
   // A segment ends at tile t when t is its unit's last or the share's last tile. Its
   // partial goes through the out slot unless tile t - 1 ended one too (the slot may
   // still be read then); the consumers then store it themselves.
@@ -1812,6 +1825,30 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     bool pc_prev_end = false;
     HeldPartial<D, W> held;
     int64_t held_slot = -1;  // >= 0: a partial is held for the end
+    // A line tile's page ids and K/V loads: with double tiles, its two 32-position stages
+    // (the cursor's tile index counted in 32-position tiles for them).
+    auto ids_of = [&](const Cursor &c, char *st) {
+      if constexpr (DBL) {
+        Cursor c2 = c;
+        c2.lt = 2 * c.lt;
+        issue_ids<LAYOUT, D, F8>(a, table, c2, st, lane);
+        c2.lt += 1;
+        issue_ids<LAYOUT, D, F8>(a, table, c2, st + G::STAGE, lane);
+      } else {
+        issue_ids<LAYOUT, D, F8>(a, table, c, st, lane);
+      }
+    };
+    auto kv_of = [&](char *st) {
+      if constexpr (DBL) {
+        Loader l2 = ld;
+        l2.c.lt = 2 * ld.c.lt;
+        issue_kv<LAYOUT, D, 1, F8, krow<LAYOUT, D, F8, W>()>(a, l2, st, 0, lane, loff);
+        l2.c.lt += 1;
+        issue_kv<LAYOUT, D, 1, F8, krow<LAYOUT, D, F8, W>()>(a, l2, st + G::STAGE, 0, lane, loff);
+      } else {
+        issue_kv<LAYOUT, D, 1, F8, krow<LAYOUT, D, F8, W>()>(a, ld, st, 0, lane, loff);
+      }
+    };
     auto handoff = [&](int t) {  // after the barrier that follows tile t
       const bool end = pc.lt == pc.tiles - 1 || t == ntiles - 1;
       if (end && !pc_prev_end) {
@@ -1827,16 +1864,16 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
     };
     if (IDS) {
       for (int j = 0; j < S && j < ntiles; ++j) {
-        issue_ids<LAYOUT, D, F8>(a, table, ct, stage(j), lane);
+        ids_of(ct, stage(j));
         if (j + 1 < ntiles) cursor_next(a, sm, ct);
       }
       wait_vm<0>();
     }
     for (int j = 0; j < S - 1 && j < ntiles; ++j) {
-      issue_kv<LAYOUT, D, 1, F8, krow<LAYOUT, D, F8, W>()>(a, ld, stage(j), 0, lane, loff);
+      kv_of(stage(j));
       if (j + 1 < ntiles) loader_advance<LAYOUT, G::ES>(a, sm, ld);
       if (IDS && j + S <= 2 * S - 3 && j + S < ntiles) {
-        issue_ids<LAYOUT, D, F8>(a, table, ct, stage(j + S), lane);
+        ids_of(ct, stage(j + S));
         cursor_next(a, sm, ct);
       }
     }
@@ -1847,16 +1884,16 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       if (i < ntiles) {
         const int later = ntiles - 1 - i;
         if (IDS && later >= 2 * S - 3) {
-          wait_vm<(G::NI + 1) * (S - 2)>();
+          wait_vm<(GN + GI) * (S - 2)>();
         } else if (IDS) {
-          int nwait = G::NI * (later < S - 2 ? later : S - 2);
+          int nwait = GN * (later < S - 2 ? later : S - 2);
           const int ids = later - (S - 1);  // tiles at or after i + S
-          nwait += ids <= 0 ? 0 : (ids < S - 2 ? ids : S - 2);
+          nwait += GI * (ids <= 0 ? 0 : (ids < S - 2 ? ids : S - 2));
           wait_vm(nwait);
         } else if (later >= S - 2) {
-          wait_vm<G::NI *(S - 2)>();
+          wait_vm<GN *(S - 2)>();
         } else if (S > 3 && later == 1) {
-          wait_vm<G::NI>();
+          wait_vm<GN>();
         } else {
           wait_vm<0>();
         }
@@ -1866,10 +1903,10 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       if (i >= ntiles) continue;
       if (i + S - 1 < ntiles) {
         if (IDS && i + 2 * S - 2 < ntiles) {
-          issue_ids<LAYOUT, D, F8>(a, table, ct, stage(i + 2 * S - 2), lane);
+          ids_of(ct, stage(i + 2 * S - 2));
           cursor_next(a, sm, ct);
         }
-        issue_kv<LAYOUT, D, 1, F8, krow<LAYOUT, D, F8, W>()>(a, ld, stage(i + S - 1), 0, lane, loff);
+        kv_of(stage(i + S - 1));
         if (i + S < ntiles) loader_advance<LAYOUT, G::ES>(a, sm, ld);
       }
     }
@@ -2023,7 +2060,12 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
       l = 0.f;
     }
     }
-    compute_tile<D, F8, krow<LAYOUT, D, F8, W>()>(a, stage(i), qf, sl, acc, m, l, cc.lt * G::T, cc.L, lane);
+    compute_tile<D, F8, krow<LAYOUT, D, F8, W>()>(a, stage(i), qf, sl, acc, m, l, cc.lt * TL, cc.L, lane);
+    if constexpr (DBL) {  // the line tile's second 32 positions, where the sequence reaches them
+      if (cc.lt * TL + G::T < cc.L)
+        compute_tile<D, F8, krow<LAYOUT, D, F8, W>()>(a, stage(i) + G::STAGE, qf, sl, acc, m, l,
+                                                      cc.lt * TL + G::T, cc.L, lane);
+    }
     const bool end = cc.lt == cc.tiles - 1 || i == ntiles - 1;
     if (DQ && end && dma_issued) {
       // The next unit's records in place before the barrier that opens it (this
@@ -2590,7 +2632,8 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->rp = row_plan(hq / hkv, q_len);
   AttnKernel k = select_kernel(layout, d, sz->rp.nrb, qmode);
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
-  const int tile = is_f8(qmode) ? TILE_F8 : TILE;
+  const bool t64 = is_f8(qmode) || (small_tiles == 0 && double_tiles(sz->rp.nrb, false));
+  const int tile = t64 ? TILE_F8 : TILE;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + tile - 1) / tile);
   const Tuning &tu = tuning();
   const int min_tiles = tuned(tu.min_tiles, 8) > 0 ? tuned(tu.min_tiles, 8) : 1;
@@ -2800,8 +2843,10 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // the cut, and an extra cost only unbalances shares of equal units (batch 8 of
   // 32768-position sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
   // FLASHMAP_SHARE_COST overrides.
+  a.t64 = a.f8 || (small_tiles == 0 && double_tiles(sz.rp.nrb, false));
   const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares
-                          ? (qmode == Q_F8_DIRECT ? 10 : a.f8 ? 4 : qmode == Q_DIRECT ? 6 : 2)
+                          ? (qmode == Q_F8_DIRECT ? 10 : a.f8 ? 4 : a.t64 ? (qmode == Q_DIRECT ? 3 : 1)
+                                                                          : qmode == Q_DIRECT ? 6 : 2)
                           : 0;
   a.share_c = small_tiles > 0 ? 0 : tuned(tuning().share_cost, share_c);
   if (a.share_c < 0) a.share_c = 0;
@@ -2827,10 +2872,10 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
       }
       plan = own;
     }
-    a.plan = plan + (a.f8 ? c.batch + 1 : 0);  // the prefix of this call's tile size
+    a.plan = plan + (a.t64 ? c.batch + 1 : 0);  // the prefix of this call's tile size
   } else {
     a.plan = nullptr;
-    a.uniform_tiles = (a.uniform_len + (a.f8 ? TILE_F8 : TILE) - 1) / (a.f8 ? TILE_F8 : TILE);
+    a.uniform_tiles = (a.uniform_len + (a.t64 ? TILE_F8 : TILE) - 1) / (a.t64 ? TILE_F8 : TILE);
   }
   const int64_t qblocks = (units * sz.rp.nrb + 3) / 4 + (a.plan_out != nullptr ? 1 : 0);
   const VerifyArgs nov{};
