@@ -135,6 +135,38 @@ def test_paged_vllm_matches_oracle_and_contig(dev, hq, hkv, page):
     assert torch.equal(got.view(b, t, hq, d), contig), "paged and contiguous layouts must agree bit for bit"
 
 
+@pytest.mark.parametrize("hq,hkv", [(64, 8), (56, 8), (48, 8)])
+def test_one_replica_double_tiles(dev, hq, hkv):
+    """Units of 6-8 row blocks run one replica per workgroup with 64-position line tiles
+    (two 32-position stages each): lengths on either side of every 32- and 64-position
+    boundary (the second stage empty, partial or full), and a long one; against the oracle,
+    and paged == contiguous bit for bit, and the token pool (SGLang) against the oracle."""
+    g = gen(61)
+    d, t, page = 128, 16, 16
+    lens = torch.tensor([1, 31, 32, 33, 63, 64, 65, 95, 96, 97, 129, 0, 513, 1000])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    want = ref.block_attention_paged_vllm(q, cache, cu, lens, bt)
+    o = ops()
+    got = o.block_attention_paged(
+        q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), t, lmax, d ** -0.5
+    )
+    check_close(got, want)
+    contig = o.block_attention_contig(q.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev), seqlens_k=lens.to(dev))
+    assert torch.equal(got.view(b, t, hq, d), contig), "paged and contiguous layouts must agree bit for bit"
+    kp, vp, pt = token_pool_from_contig(k, v, lens, g)
+    want_p = ref.block_attention_token_paged(q.view(b, t, hq, d), kp, vp, lens, pt)
+    got_p = o.block_attention_token_paged(q.view(b, t, hq, d).to(dev), kp.to(dev), vp.to(dev),
+                                          lens.to(dev, torch.int32), pt.to(dev))
+    check_close(got_p, want_p)
+
+
 def test_paged_zero_length_gives_zeros(dev):
     g = gen(7)
     hq, hkv, d, t, page = 8, 2, 128, 16, 16
