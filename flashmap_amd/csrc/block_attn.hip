@@ -73,16 +73,21 @@ constexpr int MAX_RUNS = 8;   // paged: runs of KV heads over several caches
 // wavefront in lockstep: co-resident workgroups would instead be served oldest-first, and
 // with equal static shares the youngest would finish last, leaving a tail with a
 // fraction of the loads in flight. Two replicas while the workgroup stays within 12
-// wavefronts (3 per SIMD, so up to 168 VGPRs each).
-__host__ __device__ constexpr int replicas(int w) { return 2 * (w + 1) <= 12 ? 2 : 1; }
+// wavefronts (3 per SIMD, so up to 168 VGPRs each); for bf16 K/V in pages of 16 or more
+// (or contiguous) up to 4 row blocks: at 5 (GQA 5) one replica streaming 64-position line
+// tiles (below) measured faster (C5 kernel 131.0 -> 128.8 us, combine 7.3 -> 6.7 us). On
+// token pools the two-replica kernel's K staged by rows wins (verify, 68 rows: 193 us
+// against 218 us with one replica).
+enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
+__host__ __device__ constexpr int replicas(int w, bool f8 = false, int layout = PAGED16) {
+  return 2 * (w + 1) <= (f8 || layout == PAGED ? 12 : 10) ? 2 : 1;
+}
 
-// bf16 one-replica workgroups (W >= 6 row blocks) stream 64-position line tiles, each ring
+// bf16 one-replica workgroups (W >= 5 row blocks) stream 64-position line tiles, each ring
 // slot holding two 32-position stages: the barrier cycle costs about the same at every
 // tile size (the producer's page ids and hand-off, the consumers' bookkeeping), so one
 // replica moves twice the bytes per cycle (two replicas already move two tiles).
-__host__ __device__ constexpr bool double_tiles(int w, bool f8) { return !f8 && replicas(w) == 1; }
-
-enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
+__host__ __device__ constexpr bool double_tiles(int w, bool f8, int layout) { return !f8 && replicas(w, f8, layout) == 1; }
 
 // K/V geometry of the units.
 struct UnitArgs {
@@ -539,7 +544,7 @@ __device__ __forceinline__ void loader_advance(const AttnArgs &a, const SeqMeta<
 // drafting) got 13 % slower with it, and vLLM's 16-position pages (whose sixteen rows lie
 // 512 bytes apart in one page) 2 % slower: both keep the MFMA-ordered stage.
 template <int LAYOUT, int D, bool F8, int W>
-__host__ __device__ constexpr bool krow() { return LAYOUT == PAGED && D == 128 && replicas(W) == 2; }
+__host__ __device__ constexpr bool krow() { return LAYOUT == PAGED && D == 128 && replicas(W, F8, LAYOUT) == 2; }
 
 // Row (within the tile) and byte offset within the row of this lane's k-th load of a
 // tile, and whether it is a K load. Load i = wave + k*W of the NI loads (K blocks, then
@@ -1456,11 +1461,12 @@ __device__ __forceinline__ void lds_publish() { asm volatile("s_waitcnt lgkmcnt(
 // two shares or fewer), where every share starts about one segment and a launch is saved.
 constexpr int QTOK = 16;
 
-template <int D, int W, bool F8, bool DQ>
+template <int LAYOUT, int D, int W, bool F8, bool DQ>
 __host__ __device__ constexpr int kernel_seq_cap() {
   using G = Geo<D, F8>;
-  constexpr int ring = G::SMEM * (double_tiles(W, F8) ? 2 : 1);
-  constexpr int fixed = replicas(W) * (ring + OutSlot<D, W>::BYTES) + (DQ ? replicas(W) * QTOK * D * 4 + D * 4 : 0);
+  constexpr int R = replicas(W, F8, LAYOUT);
+  constexpr int ring = G::SMEM * (double_tiles(W, F8, LAYOUT) ? 2 : 1);
+  constexpr int fixed = R * (ring + OutSlot<D, W>::BYTES) + (DQ ? R * QTOK * D * 4 + D * 4 : 0);
   constexpr int per = 8 + (DQ ? 8 + 4 * QTOK : 0);  // (prefix, length); (first token, rows) and rope rows
   constexpr int cap = (163840 - fixed - 1024) / per - 1;
   return cap < SEQ_LDS ? cap : SEQ_LDS;
@@ -1691,7 +1697,7 @@ __device__ __forceinline__ float quantize_query_rows(const u32x4_t (&x)[D / 32],
 // i-1 back (their reads of it done), and a partial written in iteration t to the
 // producer, who stores it in iteration t + 1.
 template <int LAYOUT, int W, int D, bool F8 = false, bool DQ = false>
-__global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
+__global__ __launch_bounds__(64 * (W + 1) * replicas(W, F8, LAYOUT)) void attn_fwd_kernel(
     const AttnArgs a, const int32_t *__restrict__ table, const int32_t *__restrict__ plan,
     const int32_t *__restrict__ seqlens) {
   using G = Geo<D, F8>;
@@ -1699,15 +1705,15 @@ __global__ __launch_bounds__(64 * (W + 1) * replicas(W)) void attn_fwd_kernel(
   constexpr int QF = G::KC;                // 16-byte query fragments per lane
   constexpr int UNIT_Q = 16 * W * G::RB;   // bytes of a unit's packed query rows
   constexpr bool IDS = LAYOUT != CONTIG;  // page ids join the load stream
-  constexpr int R = replicas(W);
+  constexpr int R = replicas(W, F8, LAYOUT);
   constexpr int S = G::NS;
-  constexpr bool DBL = double_tiles(W, F8);      // two 32-position stages per line tile
+  constexpr bool DBL = double_tiles(W, F8, LAYOUT);  // two 32-position stages per line tile
   constexpr int SUB = DBL ? 2 : 1;
   constexpr int TL = SUB * G::T;                 // positions per line tile
   constexpr int SLOT = SUB * G::STAGE;           // bytes per ring slot
   constexpr int GN = SUB * G::NI, GI = SUB;      // loads and page-id loads per line tile
   constexpr int RBYTES = S * SLOT + O::BYTES;    // per replica: the ring, then the out slot
-  constexpr int SEQ = kernel_seq_cap<D, W, F8, DQ>();  // sequences whose metadata is staged in LDS
+  constexpr int SEQ = kernel_seq_cap<LAYOUT, D, W, F8, DQ>();  // sequences whose metadata is staged in LDS
   constexpr int RBUF = QTOK * D * 4;                  // DQ: a replica's rope buffer
   static_assert(S >= 3, "the wait schedule keeps one group between tiles");
   static_assert((S - 2) * GN + (S - 2) * GI < 64, "vmcnt holds 6 bits");
@@ -2487,18 +2493,25 @@ enum QMode { Q_DIRECT = 0, Q_PACKED = 1, Q_F8 = 2, Q_F8_DIRECT = 3 };
 static bool is_f8(int qmode) { return qmode == Q_F8 || qmode == Q_F8_DIRECT; }
 static bool has_pass(int qmode) { return qmode == Q_PACKED || qmode == Q_F8; }
 
-template <int D, bool F8>
+template <int LAYOUT, int D, bool F8>
 static int dq_seq_cap(int w) {
   switch (w) {
-    case 1: return kernel_seq_cap<D, 1, F8, true>();
-    case 2: return kernel_seq_cap<D, 2, F8, true>();
-    case 3: return kernel_seq_cap<D, 3, F8, true>();
-    case 4: return kernel_seq_cap<D, 4, F8, true>();
-    case 5: return kernel_seq_cap<D, 5, F8, true>();
-    case 6: return kernel_seq_cap<D, 6, F8, true>();
-    case 7: return kernel_seq_cap<D, 7, F8, true>();
-    default: return kernel_seq_cap<D, 8, F8, true>();
+    case 1: return kernel_seq_cap<LAYOUT, D, 1, F8, true>();
+    case 2: return kernel_seq_cap<LAYOUT, D, 2, F8, true>();
+    case 3: return kernel_seq_cap<LAYOUT, D, 3, F8, true>();
+    case 4: return kernel_seq_cap<LAYOUT, D, 4, F8, true>();
+    case 5: return kernel_seq_cap<LAYOUT, D, 5, F8, true>();
+    case 6: return kernel_seq_cap<LAYOUT, D, 6, F8, true>();
+    case 7: return kernel_seq_cap<LAYOUT, D, 7, F8, true>();
+    default: return kernel_seq_cap<LAYOUT, D, 8, F8, true>();
   }
+}
+
+// Sequences a direct-rows kernel stages in LDS, for a call's layout and head_dim.
+template <bool F8>
+static int dq_cap(int layout, int d, int w) {
+  if (layout == PAGED) return d == 128 ? dq_seq_cap<PAGED, 128, F8>(w) : dq_seq_cap<PAGED, 64, F8>(w);
+  return d == 128 ? dq_seq_cap<PAGED16, 128, F8>(w) : dq_seq_cap<PAGED16, 64, F8>(w);
 }
 
 template <int LAYOUT, int D>
@@ -2632,12 +2645,12 @@ static int sizing(int layout, int batch, int q_len, int hq, int hkv, int d, int 
   sz->rp = row_plan(hq / hkv, q_len);
   AttnKernel k = select_kernel(layout, d, sz->rp.nrb, qmode);
   const int64_t ups = (int64_t)hkv * sz->rp.rgroups;
-  const bool t64 = is_f8(qmode) || (small_tiles == 0 && double_tiles(sz->rp.nrb, false));
+  const bool t64 = is_f8(qmode) || (small_tiles == 0 && double_tiles(sz->rp.nrb, false, layout));
   const int tile = t64 ? TILE_F8 : TILE;
   const int64_t tiles_bound = ups * batch * (((int64_t)max_k + tile - 1) / tile);
   const Tuning &tu = tuning();
   const int min_tiles = tuned(tu.min_tiles, 8) > 0 ? tuned(tu.min_tiles, 8) : 1;
-  const int r = replicas(sz->rp.nrb);
+  const int r = replicas(sz->rp.nrb, is_f8(qmode), layout);
   int64_t nw = (int64_t)info.cus * occupancy(k, 64 * (sz->rp.nrb + 1) * r);
   const int cap = tuned(tu.workgroups, 0);
   if (cap > 0) nw = cap;
@@ -2758,7 +2771,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     const bool inter = c.rope_ps == 2 && c.rope_sin == c.rope_cos + 1;
     const bool fast_rope = c.qn_w == nullptr || ((split || inter) && ((uintptr_t)c.rope_cos & 15) == 0 &&
                                                  c.rope_rs % 4 == 0 && ((uintptr_t)c.qn_w & 3) == 0);
-    const int cap = c.d == 128 ? dq_seq_cap<128, false>(rp.nrb) : dq_seq_cap<64, false>(rp.nrb);
+    const int cap = dq_cap<false>(layout, c.d, rp.nrb);
     // Direct rows cost a prologue at every segment start, inside the workgroup's barrier
     // cycle (about 5000 shader cycles at 64 rows x D 128), which the cost cut of the line
     // absorbs (6 tiles per unit); the query pass costs a launch and one read + write of the
@@ -2784,7 +2797,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     const bool inter = c.rope_ps == 2 && c.rope_sin == c.rope_cos + 1;
     const bool fast_rope = c.qn_w == nullptr || ((split || inter) && ((uintptr_t)c.rope_cos & 15) == 0 &&
                                                  c.rope_rs % 4 == 0 && ((uintptr_t)c.qn_w & 3) == 0);
-    const int cap = c.d == 128 ? dq_seq_cap<128, true>(rp.nrb) : dq_seq_cap<64, true>(rp.nrb);
+    const int cap = dq_cap<true>(layout, c.d, rp.nrb);
     const int force = tuned(tuning().query_pass, -1);
     if (fast_rope && c.batch <= cap && force == 0) qmode = Q_F8_DIRECT;
   }
@@ -2843,7 +2856,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // the cut, and an extra cost only unbalances shares of equal units (batch 8 of
   // 32768-position sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
   // FLASHMAP_SHARE_COST overrides.
-  a.t64 = a.f8 || (small_tiles == 0 && double_tiles(sz.rp.nrb, false));
+  a.t64 = a.f8 || (small_tiles == 0 && double_tiles(sz.rp.nrb, false, layout));
   const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares
                           ? (qmode == Q_F8_DIRECT ? 10 : a.f8 ? 4 : a.t64 ? (qmode == Q_DIRECT ? 3 : 1)
                                                                           : qmode == Q_DIRECT ? 6 : 2)
@@ -2896,7 +2909,7 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   }
   if (pass) FM_CHECK_HIP(hipGetLastError());
   AttnKernel k = small_tiles > 0 ? select_small(layout, c.d, sz.rp.nrb) : select_kernel(layout, c.d, sz.rp.nrb, qmode);
-  const dim3 kblock(small_tiles > 0 ? 64 * (sz.rp.nrb + 1) : 64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb));
+  const dim3 kblock(small_tiles > 0 ? 64 * (sz.rp.nrb + 1) : 64 * (sz.rp.nrb + 1) * replicas(sz.rp.nrb, a.f8 != 0, layout));
   const int32_t *ktab = a.table, *kplan = a.plan, *kseq = a.seqlens;
   void *kargs[] = {&a, &ktab, &kplan, &kseq};
   profile_before(c.stream);
@@ -3132,7 +3145,7 @@ extern "C" int fm_static_scratch_init(void) {
     for (int layout : {(int)PAGED16, (int)PAGED})
       for (int w = 1; w <= NRB_MAX; ++w)
         for (int qmode : {(int)Q_DIRECT, (int)Q_PACKED})
-          occupancy(select_kernel(layout, d, w, qmode), 64 * (w + 1) * replicas(w));
+          occupancy(select_kernel(layout, d, w, qmode), 64 * (w + 1) * replicas(w, false, layout));
   return FM_OK;
 }
 
