@@ -411,6 +411,55 @@ def test_direct_rows_equal_query_pass(dev, tuning, kind, layout):
 
 
 @pytest.mark.parametrize("layout", ["contig", "paged"])
+@pytest.mark.parametrize("hq,hkv", [(40, 8), (48, 8), (64, 8)])
+@pytest.mark.parametrize("workgroups", ["6", ""])
+def test_one_replica_direct_rows_equal_query_pass(dev, tuning, layout, hq, hkv, workgroups):
+    """One-replica workgroups (GQA 5-8: 64-position line tiles) with direct rows, with few
+    workgroups (long shares, several units and segment starts each) and with the default
+    split: the same bits as the query pass, and the oracle's attention."""
+    g = gen(43)
+    d, t, page = 128, 16, 16
+    lens = torch.tensor([1500, 700, 33, 1, 260, 95])
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q_pre = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table, make = _tables("interleaved", lmax + t + 1, d)
+    rope = make(table.to(dev))
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    pos = torch.cat([int(n) + torch.arange(t) for n in lens])
+    o = ops()
+    pro = o.Prologue(w.to(dev), rope, pos.to(dev), 1e-6)
+    if layout == "paged":
+        bt, total = paged_layout(lens, page, g)
+        cache = vllm_cache_from_contig(k, v, lens, page, bt, total).to(dev)
+
+        def run():
+            return o.block_attention_paged(q_pre.to(dev), cache, cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), t,
+                                           lmax, d ** -0.5, prologue=pro)
+    else:
+        def run():
+            return o.block_attention_contig(q_pre.view(b, t, hq, d).to(dev), k.to(dev), v.to(dev),
+                                            seqlens_k=lens.to(dev), prologue=pro)
+    tuning("FLASHMAP_SMALL_TILES", "0")
+    tuning("FLASHMAP_SHARE_COST", "2")
+    tuning("FLASHMAP_SPLITKV_WORKGROUPS", workgroups)
+    outs = {}
+    for mode in ("1", "0"):
+        tuning("FLASHMAP_QUERY_PASS", mode)
+        outs[mode] = run()
+    assert torch.equal(outs["0"], outs["1"]), f"{hq}/{hkv} {layout}: direct rows differ from the query pass"
+    qn = ref.rms_norm_rope_vllm(q_pre, w, table, pos, 1e-6)
+    got = outs["0"].cpu().view(-1, hq, d)
+    for i in range(b):
+        s, e = i * t, (i + 1) * t
+        want = ref.attention(qn[s:e].transpose(0, 1), k[i, :, : int(lens[i])], v[i, :, : int(lens[i])])
+        check_close(got[s:e], want.transpose(0, 1))
+
+
+@pytest.mark.parametrize("layout", ["contig", "paged"])
 @pytest.mark.parametrize("hq,hkv,lens", [(8, 2, [700, 33, 0, 260]), (32, 8, [1100, 5])])
 def test_small_call_kernel(dev, tuning, layout, hq, hkv, lens):
     """Calls whose K/V fits one pass of a few-tile workgroups over the CUs run the small-call
