@@ -1036,6 +1036,42 @@ __device__ __forceinline__ void plan_prefixes(const int32_t *__restrict__ seqlen
   }
 }
 
+// One query row per lane group (lane (n, g): channels 32 t + 8 g .. + 7 of its row) read
+// from src, QK-RMSNormed and rotated when a.qn_w is set (at the rotary row of position
+// a.q_pos[tok], or tok). A row with ok false reads nothing. The norm weights are issued
+// first, so that they, the row and its position take one memory round trip and the
+// rotary row (addressed by the position) a second. ALL: every row of the wavefront is
+// valid and no load is conditional; a conditional load is joined with zeros after it, and
+// the join had the compiler wait for each such load before issuing the next.
+template <int D, bool ALL>
+__device__ __forceinline__ void query_row(const AttnArgs &a, u32x4_t (&x)[D / 32], const uint16_t *src, bool ok,
+                                          int64_t tok, int g) {
+  constexpr int KT = D / 32;
+  const bool in = ALL || ok;
+  if (a.qn_w != nullptr) {
+    PrologueOps<D> ops;
+    load_norm_ops<D>(ops, a.qn_w, g);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) x[t] = in ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
+    const int64_t rr = clamp_row(a.rope, in ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
+    load_rope_ops<D>(ops, a.rope, rr, g);
+    norm_rope_apply<D>(x, ops, a.eps);  // every lane: the norm crosses lane groups
+  } else {
+#pragma unroll
+    for (int t = 0; t < KT; ++t) x[t] = in ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
+  }
+}
+
+// query_row with ALL chosen at run time: true when no active lane's row is invalid.
+template <int D>
+__device__ __forceinline__ void query_row_any(const AttnArgs &a, u32x4_t (&x)[D / 32], const uint16_t *src, bool ok,
+                                              int64_t tok, int g) {
+  if (__builtin_amdgcn_ballot_w64(!ok) == 0)
+    query_row<D, true>(a, x, src, ok, tok, g);
+  else
+    query_row<D, false>(a, x, src, ok, tok, g);
+}
+
 // The query rows of every unit in MFMA-block order: row r of unit (b, h, rg) is query
 // head h*G + R / q_len at draft token R % q_len, R = rg * 16 nrb + r, rows beyond the
 // group or the sequence's draft rows are zero. With the prologue requested, each row
@@ -1069,12 +1105,7 @@ __global__ __launch_bounds__(256) void pack_queries_kernel(const AttnArgs a, con
   const uint16_t *src = a.q + (a.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)(valid ? tq : 0) * a.q_st) +
                         head * a.q_sh + 8 * g;
   u32x4_t qf[KT];
-#pragma unroll
-  for (int t = 0; t < KT; ++t) qf[t] = valid ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
-  if (a.qn_w != nullptr) {
-    const int64_t rr = clamp_row(a.rope, valid ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
-    norm_rope_row<D>(qf, a.qn_w, a.eps, a.rope, rr, g);
-  }
+  query_row_any<D>(a, qf, src, valid, tok, g);
   uint16_t *dst = const_cast<uint16_t *>(a.qp) + (unit * 16 * a.nrb + r) * D + 8 * g;
 #pragma unroll
   for (int t = 0; t < KT; ++t) store16_nt(dst + 32 * t, valid ? qf[t] : u32x4_t{0, 0, 0, 0});
@@ -1133,13 +1164,7 @@ __global__ __launch_bounds__(256) void pack_queries_f8_kernel(const AttnArgs a) 
   } else {
     auto load_row = [&](int t_, bool ok, u32x4_t (&x)[KT]) {  // every lane calls it (the norm crosses lanes)
       const uint16_t *src = a.q + row_src(ok ? t_ : 0) + 8 * g;
-#pragma unroll
-      for (int t = 0; t < KT; ++t) x[t] = ok ? load16(src + 32 * t) : u32x4_t{0, 0, 0, 0};
-      if (a.qn_w != nullptr) {
-        const int64_t tok = q_token_index(a, b, ok ? t_ : 0);
-        const int64_t rr = clamp_row(a.rope, ok ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
-        norm_rope_row<D>(x, a.qn_w, a.eps, a.rope, rr, g);
-      }
+      query_row_any<D>(a, x, src, ok, q_token_index(a, b, ok ? t_ : 0), g);
 #pragma unroll
       for (int t = 0; t < KT; ++t)
         if (!ok) x[t] = u32x4_t{0, 0, 0, 0};
@@ -2116,7 +2141,6 @@ template <int D>
 __device__ __forceinline__ void small_query_rows(const AttnArgs &a, int64_t unit, int r, int g,
                                                  u32x4_t (&qf)[D / 32]) {
   constexpr int KT = D / 32;
-  typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
   const int b = (int)(unit / a.ups);
   const int ul = (int)(unit - (int64_t)b * a.ups);
   const int h = ul / a.rgroups, rg = ul - h * a.rgroups;
@@ -2127,12 +2151,7 @@ __device__ __forceinline__ void small_query_rows(const AttnArgs &a, int64_t unit
   const int64_t head = (int64_t)h * a.group + (valid ? gq : 0);
   const uint16_t *src = a.q + (a.cu_q ? tok * a.q_st : (int64_t)b * a.q_sb + (int64_t)(valid ? tq : 0) * a.q_st) +
                         head * a.q_sh + 8 * g;
-#pragma unroll
-  for (int t = 0; t < KT; ++t) qf[t] = valid ? *(g_u32x4_t *)(src + 32 * t) : u32x4_t{0, 0, 0, 0};
-  if (a.qn_w != nullptr) {
-    const int64_t rr = clamp_row(a.rope, valid ? (a.q_pos ? a.q_pos[tok] : tok) : 0);
-    norm_rope_row<D>(qf, a.qn_w, a.eps, a.rope, rr, g);  // every lane: the norm crosses lanes
-  }
+  query_row_any<D>(a, qf, src, valid, tok, g);
 #pragma unroll
   for (int t = 0; t < KT; ++t)
     if (!valid) qf[t] = u32x4_t{0, 0, 0, 0};

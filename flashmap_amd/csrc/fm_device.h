@@ -189,9 +189,11 @@ __device__ __forceinline__ void load_rope_ops(PrologueOps<D> &ops, const Rope &r
   }
 }
 
+// The norm weights of this lane's channels into ops.w. They depend on no row, so a
+// caller whose rotary row waits on a loaded position issues them first: they then share
+// the first memory round trip instead of adding one after the position arrives.
 template <int D>
-__device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const float *__restrict__ w,
-                                                  const Rope &rope, int64_t rope_row, int g) {
+__device__ __forceinline__ void load_norm_ops(PrologueOps<D> &ops, const float *__restrict__ w, int g) {
   constexpr int KT = D / 32;
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
@@ -203,6 +205,12 @@ __device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const flo
       ops.w[t][4 + q] = hi[q];
     }
   }
+}
+
+template <int D>
+__device__ __forceinline__ void load_prologue_ops(PrologueOps<D> &ops, const float *__restrict__ w,
+                                                  const Rope &rope, int64_t rope_row, int g) {
+  load_norm_ops<D>(ops, w, g);
   load_rope_ops<D>(ops, rope, rope_row, g);
 }
 
