@@ -229,6 +229,36 @@ def test_paged_fp8_own_plan_equals_step_plan(dev):
     assert torch.equal(own, step)
 
 
+@pytest.mark.parametrize("q_len", [16, 32])
+def test_paged_fp8_call_quantization_equals_callers(dev, q_len):
+    """bf16 queries quantized inside the call (per (request, query head): scale = max(amax,
+    1e-12) / 448, q / scale rounded to nearest even; flashmap/sglang/model.py:167-169) give
+    the bits of the same queries quantized on the CPU by the oracle (float32 division,
+    torch's e4m3 conversion) and passed as e4m3 with that scale as the query descale:
+    the call's scale and codes equal the CPU's exactly. One query head per KV head, so
+    that the descales' (request, KV head) grid holds every head's scale. Heads span 1e-14
+    (below the 1e-12 floor) to 1e3, and one is all zeros."""
+    print(f"fp8 call quantization q_len={q_len}", flush=True)
+    g = gen(99 + q_len)
+    bs, h, d, page = 4, 8, 128, 16
+    lens = torch.tensor([37, 600, 0, 255])
+    bt, total = paged_layout(lens.tolist(), page, g)
+    cache = _e4m3((total, h, page, 2 * d), g)
+    mag = torch.tensor([1e-3, 3.0, 1e3, 0.0, 1e-14, 0.25, 40.0, 1.0])
+    q = (torch.randn(bs, q_len, h, d, generator=g) * mag[None, None, :, None]).bfloat16()
+    q8, qscale = ref.quantize_query_per_head(q)  # (bs, T, H, D) e4m3, (bs, H)
+    kv_desc = torch.rand(2, bs, h, generator=g) + 0.25
+    cu = torch.arange(0, bs * q_len + 1, q_len, dtype=torch.int32)
+    args = (cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev), q_len, 600, d ** -0.5)
+    in_call = ops().block_attention_paged_fp8(q.view(-1, h, d).to(dev), *args,
+                                              descales=torch.cat([torch.ones(1, bs, h), kv_desc]).to(dev))
+    by_caller = ops().block_attention_paged_fp8(q8.view(-1, h, d).to(dev), *args,
+                                                descales=torch.cat([qscale[None], kv_desc]).to(dev))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(by_caller[2 * q_len:3 * q_len]) == 0  # a request without context
+    assert torch.equal(in_call.cpu(), by_caller.cpu())
+
+
 @pytest.mark.parametrize("descales", [False, True])
 @pytest.mark.parametrize("layout,d,hq,hkv", [("paged", 128, 32, 8), ("pool", 128, 32, 8), ("paged", 64, 8, 2),
                                             ("pool", 64, 40, 8)])
