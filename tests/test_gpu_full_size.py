@@ -1,7 +1,8 @@
 """The benchmark configurations at their full sizes on the GPU (C3: 64 x U[256, 8192]; C4:
 8 x 32768; C5: GQA 5, 32 x U[1024, 8192]; R8B: MHA 16/16, 64 x U[256, 8192]; vLLM pages of
-16), checked through properties that hold at any size, since the oracle over a whole batch
-would take minutes:
+16; and LONG, 2 x 131072, each unit split over about 32 shares, the combine merging
+them in four batches of eight), checked through properties that hold at any size, since the
+oracle over a whole batch would take minutes:
 
 - sampled sequences (the shortest, a median one, the longest) against the float32 oracle
   on the same K/V (max-abs 2e-2, mean-abs 2e-3);
@@ -25,6 +26,7 @@ CONFIGS = {
     "C4": (8, 32, 8, 32768, 32768),
     "C5": (32, 40, 8, 1024, 8192),
     "R8B": (64, 16, 16, 256, 8192),
+    "LONG": (2, 32, 8, 131072, 131072),
 }
 K_ROWS, D, PAGE = 16, 128, 16
 
