@@ -359,6 +359,127 @@ def run_select(args, dev) -> dict:
     return result
 
 
+# The K side and the block self-attention, each as one launch over a draft step's data:
+# "kv-write-c3-vllm": the context writer over C3's draw (245380 positions, 8 KV heads of
+# 128, one layer): each key k-normed and rotated at its position, key and value stored at
+# the position's slot of a vLLM cache of 16-token pages behind a permuted block table;
+# "kv-write-c3-pool": the same rows into SGLang token pools, one pool row per position at
+# a permuted location; "self-attn-8b-b64x16": the 8B drafter layer's block self-attention,
+# 64 blocks x 16 slots, 16 heads of 128, q/k RMSNorm + RoPE at the slots' positions inside.
+KERNEL_WORKLOADS = {
+    "kv-write-c3-vllm": "vllm",
+    "kv-write-c3-pool": "pool",
+    "self-attn-8b-b64x16": "self",
+}
+
+
+def run_kernel(args, dev) -> dict:
+    """One call = one launch of the writer or of the block self-attention."""
+    from flashmap_amd import ops
+    from oracle import attention as ref
+
+    kind = KERNEL_WORKLOADS[args.workload]
+    g = torch.Generator().manual_seed(0)
+    if kind == "self":
+        blocks, t, heads, d = 64, 16, 16, 128
+        qkv = torch.randn(blocks, t, 3, heads, d, generator=g).bfloat16()
+        qn, kn = 0.75 + 0.5 * torch.rand(d, generator=g), 0.75 + 0.5 * torch.rand(d, generator=g)
+        anchors = torch.randint(256, 8192, (blocks,), generator=g)
+        pos = (anchors[:, None] + 1 + torch.arange(t)).reshape(-1)
+        table = ref.rope_table(8192 + t + 1, d, 1e6)
+        qkv_d, qn_d, kn_d, pos_d = qkv.to(dev), qn.to(dev), kn.to(dev), pos.to(dev)
+        rope = ops.rope_from_table(table.to(dev))
+
+        def call():
+            ops.block_self_attention(qkv_d, qn_d, kn_d, rope, pos_d, 1e-6)
+
+        total = blocks * t * heads * d * 2 * 4 + blocks * t * (8 + 4 * d)  # qkv in, out, positions, rotary rows
+        flops = blocks * heads * 4 * t * t * d
+        what = f"block self-attention µs/call, {blocks} blocks x {t} slots, {heads} heads of {d}"
+        config = {"workload": args.workload, "blocks": blocks, "block_size": t, "heads": heads, "head_dim": d,
+                  "prologue": "q/k RMSNorm + RoPE inside the kernel"}
+    else:
+        inp = build_inputs("c3-qwen3-8b-paged-b64")
+        hkv, d, page = inp["hkv"], inp["d"], inp["page"]
+        kv, pos = inp["kv_pre"], inp["positions"]
+        tokens = kv.shape[0]
+        kn = 0.75 + 0.5 * torch.rand(1, d, generator=g)
+        kv_d, pos_d, kn_d = kv.to(dev), pos.to(dev), kn.to(dev)
+        if kind == "vllm":
+            table = ref.rope_table(inp["hi"] + 1, d, 1e6)
+            rope = ops.rope_from_table(table.to(dev))
+            cache = torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.bfloat16, device=dev)
+            ptrs = torch.tensor([cache.data_ptr()], dtype=torch.int64, device=dev)
+            slots_d = inp["slots"].to(dev)
+            strides = (cache.stride(0), cache.stride(1), cache.stride(2), d)
+
+            def call():
+                ops.write_context_kv(kv_d, pos_d, slots_d, kn_d, rope, ptrs, strides, page, 1e-6)
+        else:
+            cat = ref.rope_cat_table(inp["hi"] + 1, d, 1e6)
+            rope = ops.rope_from_cat(cat.to(dev))
+            pool = tokens + 64
+            locs = torch.randperm(pool, generator=g)[:tokens]
+            kbuf = torch.zeros(pool, hkv, d, dtype=torch.bfloat16, device=dev)
+            vbuf = torch.zeros_like(kbuf)
+            meta = torch.tensor([[kbuf.data_ptr(), vbuf.data_ptr(), kbuf.stride(0), vbuf.stride(0)]],
+                                dtype=torch.int64, device=dev)
+            rows_d, locs_d = kv_d.view(tokens, 2 * hkv * d), locs.to(dev)
+
+            def call():
+                ops.write_context_kv_pool(rows_d, meta, kn_d, rope, pos_d, locs_d, 1, hkv * d, d, 1e-6)
+
+        total = tokens * (2 * 2 * hkv * d * 2 + 16 + 4 * d)  # rows in and out, position and slot, rotary row
+        flops = None
+        what = f"context K/V write µs/call ({kind}), {tokens} positions x {hkv} KV heads of {d}"
+        config = {"workload": args.workload, "positions": tokens, "kv_heads": hkv, "head_dim": d,
+                  "layout": "vllm paged (blocks, kv_heads, 16, 2*head_dim)" if kind == "vllm"
+                  else "sglang token pools (pool, kv_heads, head_dim), permuted rows",
+                  "prologue": "k RMSNorm + RoPE of each key"}
+    timing = _measure(call, args, kernel_events=False)
+    ms = timing["ms"]
+    gbs = total / (ms * 1e-3) / 1e9
+    result = {
+        "metric": what + ", 1 GPU",
+        "value": round(ms * 1e3, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: seeded CPU draw" + (" (C3's lengths and rows)" if kind != "self" else ""),
+        "config": config,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": total,
+                     "note": "one launch per call, timed by events around the calls"
+                             + (f"; {flops / 1e6:.0f} MFLOP per call: latency-bound at this size" if flops else "")},
+        **_timing_fields(timing),
+    }
+    if not args.no_cpu_baseline:
+        if kind == "self":
+            half = table[pos.long()]
+            cos, sin = half[..., 0].view(blocks, t, d // 2), half[..., 1].view(blocks, t, d // 2)
+
+            def run(n):
+                ref.block_self_attention(qkv[:n].float(), qn, kn, cos[:n], sin[:n], 1e-6)
+
+            rec = cpu_timed(run, [1] * blocks, "us/call", "blocks", args.cpu_budget)
+        elif kind == "vllm":
+            want = [torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.bfloat16)]
+
+            def run(n):
+                ref.write_context_kv_vllm(kv[:n], pos[:n], inp["slots"][:n], kn, table, want, page, 1e-6)
+
+            rec = cpu_timed(run, [1] * tokens, "us/call", "positions", args.cpu_budget)
+        else:
+            wk = [torch.zeros(pool, hkv, d, dtype=torch.bfloat16)]
+            wv = [torch.zeros_like(wk[0])]
+            rows = kv.view(tokens, 2 * hkv * d)
+
+            def run(n):
+                ref.write_context_kv_pool(rows[:n], wk, wv, kn, cat, pos[:n], locs[:n], 1, hkv * d, d, 1e-6)
+
+            rec = cpu_timed(run, [1] * tokens, "us/call", "positions", args.cpu_budget)
+        result["cpu_baseline"] = rec
+    return result
+
+
 def _flushed(call, args, dev, flush_mb: int = 512) -> dict:
     """Timing of a latency-bound call, its K/V read from HBM: each timed call is preceded
     by a write of ``flush_mb`` MB, which evicts the 4 MB L2s and the 256 MB Infinity
@@ -1046,7 +1167,7 @@ def main() -> int:
     ap.add_argument("--workload", default="c3-qwen3-8b-paged-b64",
                     choices=sorted(WORKLOADS) + sorted(FP8_WORKLOADS) + sorted(VERIFY_WORKLOADS)
                     + sorted(VIRTUAL_WORKLOADS) + sorted(TREE_WORKLOADS) + sorted(TREE_FP8_WORKLOADS)
-                    + sorted(SELECT_WORKLOADS)
+                    + sorted(SELECT_WORKLOADS) + sorted(KERNEL_WORKLOADS)
                     + sorted(CONTIG_WORKLOADS) + sorted(DRAFT_STEP_WORKLOADS) + sorted(SGLANG_STEP_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -1080,6 +1201,9 @@ def main() -> int:
         return 0
     if args.workload in SELECT_WORKLOADS:
         print(json.dumps(run_select(args, dev)))
+        return 0
+    if args.workload in KERNEL_WORKLOADS:
+        print(json.dumps(run_kernel(args, dev)))
         return 0
     if args.workload in CONTIG_WORKLOADS:
         print(json.dumps(run_contig(args, dev)))
