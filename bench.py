@@ -365,11 +365,14 @@ def run_select(args, dev) -> dict:
 # the position's slot of a vLLM cache of 16-token pages behind a permuted block table;
 # "kv-write-c3-pool": the same rows into SGLang token pools, one pool row per position at
 # a permuted location; "self-attn-8b-b64x16": the 8B drafter layer's block self-attention,
-# 64 blocks x 16 slots, 16 heads of 128, q/k RMSNorm + RoPE at the slots' positions inside.
+# 64 blocks x 16 slots, 16 heads of 128, q/k RMSNorm + RoPE at the slots' positions inside;
+# "norm-rope-c3-q": the standalone QK-RMSNorm + RoPE (the plugins' rms_norm_rope op) over
+# C3's query rows, 64 x 16 draft tokens x 32 heads of 128, each at its position.
 KERNEL_WORKLOADS = {
     "kv-write-c3-vllm": "vllm",
     "kv-write-c3-pool": "pool",
     "self-attn-8b-b64x16": "self",
+    "norm-rope-c3-q": "norm",
 }
 
 
@@ -380,7 +383,26 @@ def run_kernel(args, dev) -> dict:
 
     kind = KERNEL_WORKLOADS[args.workload]
     g = torch.Generator().manual_seed(0)
-    if kind == "self":
+    if kind == "norm":
+        inp = build_inputs("c3-qwen3-8b-paged-b64")
+        x, d, k_rows = inp["q_pre"], inp["d"], inp["k_rows"]
+        tokens, heads = x.shape[0], x.shape[1]
+        w = 0.75 + 0.5 * torch.rand(d, generator=g)
+        pos = torch.cat([int(n) + torch.arange(k_rows) for n in inp["lens"]])
+        table = ref.rope_table(inp["hi"] + k_rows + 1, d, 1e6)
+        x_d, w_d, pos_d = x.to(dev), w.to(dev), pos.to(dev)
+        rope = ops.rope_from_table(table.to(dev))
+        out_d = torch.empty_like(x_d)
+
+        def call():
+            ops.rms_norm_rope(x_d, w_d, rope, pos_d, 1e-6, out=out_d)
+
+        total = tokens * heads * d * 2 * 2 + tokens * (8 + 4 * d)  # rows in and out, positions, rotary rows
+        flops = None
+        what = f"QK-RMSNorm + RoPE µs/call, {tokens} tokens x {heads} heads of {d}"
+        config = {"workload": args.workload, "tokens": tokens, "heads": heads, "head_dim": d,
+                  "rope": "vLLM table (positions, head_dim / 2, [cos, sin]) gathered at each token's position"}
+    elif kind == "self":
         blocks, t, heads, d = 64, 16, 16, 128
         qkv = torch.randn(blocks, t, 3, heads, d, generator=g).bfloat16()
         qn, kn = 0.75 + 0.5 * torch.rand(d, generator=g), 0.75 + 0.5 * torch.rand(d, generator=g)
@@ -452,7 +474,12 @@ def run_kernel(args, dev) -> dict:
         **_timing_fields(timing),
     }
     if not args.no_cpu_baseline:
-        if kind == "self":
+        if kind == "norm":
+            def run(n):
+                ref.rms_norm_rope_vllm(x[:n], w, table, pos[:n], 1e-6)
+
+            rec = cpu_timed(run, [1] * tokens, "us/call", "tokens", args.cpu_budget)
+        elif kind == "self":
             half = table[pos.long()]
             cos, sin = half[..., 0].view(blocks, t, d // 2), half[..., 1].view(blocks, t, d // 2)
 
