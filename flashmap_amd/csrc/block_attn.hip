@@ -74,13 +74,15 @@ constexpr int MAX_RUNS = 8;   // paged: runs of KV heads over several caches
 // with equal static shares the youngest would finish last, leaving a tail with a
 // fraction of the loads in flight. Two replicas while the workgroup stays within 12
 // wavefronts (3 per SIMD, so up to 168 VGPRs each); for bf16 K/V in pages of 16 or more
-// (or contiguous) up to 4 row blocks: at 5 (GQA 5) one replica streaming 64-position line
-// tiles (below) measured faster (C5 kernel 131.0 -> 128.8 us, combine 7.3 -> 6.7 us). On
-// token pools the two-replica kernel's K staged by rows wins (verify, 68 rows: 193 us
+// (or contiguous) up to 3 row blocks: from 4 (GQA 4 and 5) one replica streaming
+// 64-position line tiles (below) measured faster. At GQA 5: C5 kernel 131.0 -> 128.8 us,
+// combine 7.3 -> 6.7 us. At GQA 4, five alternating runs on one box: C3 175.96 -> 174.46
+// us per call (half the shares, so about half the partials to merge); C4 171.45 -> 169.28
+// us. On token pools the two-replica kernel's K staged by rows wins (verify, 68 rows: 193 us
 // against 218 us with one replica).
 enum Layout { CONTIG = 0, PAGED16 = 1, PAGED = 2 };
 __host__ __device__ constexpr int replicas(int w, bool f8 = false, int layout = PAGED16) {
-  return 2 * (w + 1) <= (f8 || layout == PAGED ? 12 : 10) ? 2 : 1;
+  return 2 * (w + 1) <= (f8 || layout == PAGED ? 12 : 8) ? 2 : 1;
 }
 
 // bf16 one-replica workgroups (W >= 5 row blocks) stream 64-position line tiles, each ring
@@ -2794,13 +2796,14 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
     // Direct rows cost a prologue at every segment start, inside the workgroup's barrier
     // cycle (about 5000 shader cycles at 64 rows x D 128), which the cost cut of the line
     // absorbs (6 tiles per unit); the query pass costs a launch and one read + write of the
-    // rows. Measured: direct rows win up to one unit per share (batch 64 x 8 KV heads, 512
-    // units over 512 shares: 176 us per call against 179 us with the pass); calls of more units than
-    // shares keep the pass. FLASHMAP_QUERY_PASS=1 forces the pass, =0 the direct rows where
-    // they apply; at one share cost both give the same bits.
+    // rows. Measured: direct rows win up to one unit per share of 32-position tiles (batch
+    // 64 x 8 KV heads, 512 units over 512 shares: 176 us per call against 179 us with the
+    // pass), or two per share of 64-position line tiles (one replica: the same 512 units over
+    // 256 shares); calls of more units keep the pass. FLASHMAP_QUERY_PASS=1 forces the pass,
+    // =0 the direct rows where they apply; at one share cost both give the same bits.
     const int force = tuned(tuning().query_pass, -1);
     const int64_t units = (int64_t)c.batch * c.hkv * rp.rgroups;
-    const bool small = units <= sz.num_shares;
+    const bool small = units <= (int64_t)sz.num_shares * (double_tiles(rp.nrb, false, layout) ? 2 : 1);
     if (fast_rope && c.batch <= cap && (force == 0 || (force < 0 && small))) qmode = Q_DIRECT;
   }
   // e4m3 K/V with bf16 queries of one 16-row block per query head: with
