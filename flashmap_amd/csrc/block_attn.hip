@@ -2874,12 +2874,13 @@ static int run_attention(const CommonIn &c, int layout, AttnArgs a, const Verify
   // A unit's extra cost when cutting the line into shares (share_first_tiles), in tiles:
   // what a segment start and a partial hand-off cost the persistent kernel, measured best
   // at 2 tiles for bf16 (32 positions) and 4 for e4m3 (64 positions). Where the units span
-  // more than four shares each on average, every share holds one or two segments whatever
+  // four or more shares each on average, every share holds one or two segments whatever
   // the cut, and an extra cost only unbalances shares of equal units (batch 8 of
-  // 32768-position sequences: 2 us slower): the line is cut by tiles, as it is for the small-call kernel.
+  // 32768-position sequences over 256 shares: 1.5-2 us slower; the 128-row tree units of 8192
+  // positions: no change): the line is cut by tiles, as it is for the small-call kernel.
   // FLASHMAP_SHARE_COST overrides.
   a.t64 = a.f8 || (small_tiles == 0 && double_tiles(sz.rp.nrb, false, layout));
-  const int share_c = small_tiles == 0 && units * 4 >= sz.num_shares
+  const int share_c = small_tiles == 0 && units * 4 > sz.num_shares
                           ? (qmode == Q_F8_DIRECT ? 10 : a.f8 ? 4 : a.t64 ? (qmode == Q_DIRECT ? 3 : 1)
                                                                           : qmode == Q_DIRECT ? 6 : 2)
                           : 0;
