@@ -586,6 +586,38 @@ def test_share_cost_cuts(dev, tuning, cost, qpass):
     check_close(got, want)
 
 
+@pytest.mark.parametrize("workgroups", ["128", "127"])
+@pytest.mark.parametrize("lens", [[2048] * 4, [2048, 1500, 64, 1999]], ids=["equal", "ragged"])
+def test_four_shares_per_unit_cut(dev, tuning, workgroups, lens):
+    """Units that span four or more shares each are cut by tiles, fewer by cost: 32 units
+    (4 sequences x 8 KV heads, one-replica workgroups, so shares = workgroups) over 128
+    shares take the tile cut, over 127 the cost cut. Either way every tile is computed once
+    and every partial merged, with equal lengths (every unit split at the same tiles) and
+    ragged ones."""
+    g = gen(53)
+    hq, hkv, d, t, page = 32, 8, 128, 16, 16
+    lens = torch.tensor(lens)
+    b = len(lens)
+    lmax = int(lens.max())
+    k = normed_keys(b, hkv, lmax, d, g)
+    v = torch.randn(b, hkv, lmax, d, generator=g).bfloat16()
+    q = torch.randn(b * t, hq, d, generator=g).bfloat16()
+    w = torch.rand(d, generator=g) + 0.5
+    table = ref.rope_table(lmax + t + 1, d, 1e6)
+    pos = torch.cat([int(n) + torch.arange(t) for n in lens])
+    bt, total = paged_layout(lens, page, g)
+    cache = vllm_cache_from_contig(k, v, lens, page, bt, total)
+    cu = torch.arange(b + 1, dtype=torch.int32) * t
+    want = ref.block_attention_paged_vllm(ref.rms_norm_rope_vllm(q, w, table, pos, 1e-6), cache, cu, lens, bt)
+    o = ops()
+    pro = o.Prologue(w.to(dev), o.rope_from_table(table.to(dev)), pos.to(dev), 1e-6)
+    tuning("FLASHMAP_SMALL_TILES", "0")
+    tuning("FLASHMAP_SPLITKV_WORKGROUPS", workgroups)
+    got = o.block_attention_paged(q.to(dev), cache.to(dev), cu.to(dev), lens.to(dev, torch.int32), bt.to(dev),
+                                  t, lmax, d ** -0.5, prologue=pro)
+    check_close(got, want)
+
+
 @pytest.mark.parametrize("qpass", ["1", "0"])
 def test_own_plan_equals_step_plan(dev, tuning, qpass):
     """A call given no step plan computes its own (in one extra workgroup of its query pass
