@@ -12,7 +12,7 @@ the float32 oracle (max-abs 2e-2, mean-abs 2e-3 on the bf16 outputs):
   U[1024, 8192]): exactly the call bench.py times -- the query prologue fused, the step
   plan computed once and passed in, the paged op over the cache the context writer
   filled -- with every sequence of the batch checked against the oracle's prologue,
-  block-table gather and attention.
+  block-table gather and attention; and C3's call on an e4m3 cache the same way.
 """
 
 import pytest
@@ -81,8 +81,9 @@ def test_c2_full_size_fused_prologue(dev):
     print(f"C2: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
 
 
-def _bench_call(dev, workload):
-    """The inputs and the output of bench.py's timed call for ``workload``."""
+def _bench_call(dev, workload, fp8=False):
+    """The inputs and the output of bench.py's timed call for ``workload`` (``fp8``: its
+    e4m3 twin, the cache written by the fp8 context writer with scales 1)."""
     import bench
 
     ops = _ops()
@@ -92,17 +93,22 @@ def _bench_call(dev, workload):
     rope = ops.rope_from_table(table.to(dev))
     w = torch.ones(d, device=dev)
     lens = inp["lens"].to(dev, torch.int32)
-    cache = torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.bfloat16, device=dev)
+    cache = torch.zeros(inp["total"], hkv, page, 2 * d, dtype=torch.uint8 if fp8 else torch.bfloat16, device=dev)
     ptrs = torch.tensor([cache.data_ptr()], dtype=torch.int64, device=dev)
-    ops.write_context_kv(inp["kv_pre"].to(dev), inp["positions"].to(dev), inp["slots"].to(dev),
-                         w[None].expand(1, d).contiguous(), rope, ptrs,
-                         (cache.stride(0), cache.stride(1), cache.stride(2), d), page, EPS)
+    writer_args = (inp["kv_pre"].to(dev), inp["positions"].to(dev), inp["slots"].to(dev),
+                   w[None].expand(1, d).contiguous(), rope, ptrs,
+                   (cache.stride(0), cache.stride(1), cache.stride(2), d), page, EPS)
+    if fp8:
+        ops.write_context_kv_fp8(*writer_args, torch.ones(1, 2, device=dev))
+    else:
+        ops.write_context_kv(*writer_args)
     qpos = torch.cat([int(n) + torch.arange(k_rows) for n in inp["lens"]])
     cu = (torch.arange(batch + 1, dtype=torch.int32) * k_rows).to(dev)
     pro = ops.Prologue(w, rope, qpos.to(dev), EPS)
     plan = ops.attention_plan(lens)
-    out = ops.block_attention_paged(inp["q_pre"].to(dev), cache, cu, lens, inp["bt"].to(dev), k_rows, inp["hi"],
-                                    d ** -0.5, prologue=pro, plan=plan)
+    call = ops.block_attention_paged_fp8 if fp8 else ops.block_attention_paged
+    out = call(inp["q_pre"].to(dev), cache, cu, lens, inp["bt"].to(dev), k_rows, inp["hi"], d ** -0.5, prologue=pro,
+               plan=plan)
     torch.cuda.synchronize()
     return inp, table, qpos, cache, out
 
@@ -126,3 +132,29 @@ def test_bench_call_every_sequence(dev, workload):
         worst = max(worst, err.max().item())
     assert out.shape == (inp["batch"] * k_rows, hq, d)
     print(f"{workload}: {inp['batch']} sequences, worst max-abs {worst:.3e}", flush=True)
+
+
+def test_bench_call_every_sequence_e4m3(dev):
+    """The e4m3 call bench.py times (c3-qwen3-8b-paged-b64-fp8): C3's draw, the cache written
+    by the fp8 context writer with scales 1, the bf16 queries normed, rotated and quantized
+    per (sequence, query head) inside the call. Every sequence against the oracle's
+    prologue, its per-head quantization (flashmap/sglang/model.py:167-169, the bits the
+    call's own are pinned to) and the attention of the dequantized operands in float32."""
+    print("bench call c3-qwen3-8b-paged-b64-fp8", flush=True)
+    inp, table, qpos, cache, out = _bench_call(dev, "c3-qwen3-8b-paged-b64", fp8=True)
+    batch, k_rows, d, hq, hkv = inp["batch"], inp["k_rows"], inp["d"], inp["hq"], inp["hkv"]
+    qn = ref.rms_norm_rope_vllm(inp["q_pre"], torch.ones(d), table, qpos, EPS)
+    q8, qs = ref.quantize_query_per_head(qn.view(batch, k_rows, hq, d))
+    qd = q8.float() * qs[:, None, :, None]  # the queries as the call's scores see them
+    bt = inp["bt"]
+    worst = 0.0
+    for b in range(batch):
+        n = int(inp["lens"][b])
+        pages = bt[b, :(n + inp["page"] - 1) // inp["page"]].long().to(dev)
+        rows = cache[pages].view(torch.float8_e4m3fn).transpose(1, 2).reshape(-1, hkv, 2 * d)[:n].float().cpu()
+        k, v = rows[..., :d].transpose(0, 1), rows[..., d:].transpose(0, 1)
+        want = ref.attention(qd[b].transpose(0, 1), k, v, d ** -0.5)
+        err = check_close(out[b * k_rows:(b + 1) * k_rows].cpu().float(), want.transpose(0, 1))
+        worst = max(worst, err.max().item())
+    assert out.shape == (batch * k_rows, hq, d)
+    print(f"c3 e4m3: {batch} sequences, worst max-abs {worst:.3e}", flush=True)
