@@ -1006,15 +1006,13 @@ def _time_call(call, args) -> tuple[float, float, dict]:
     return t["ms"], t["kernel_ms"], t
 
 
-def run_tree(args, dev) -> dict:
-    """One call = flashmap_sglang::paged_cross_attention of every request's candidates
-    side by side: query packing, the split-KV stream and the combine."""
-    from flashmap_amd import ops
-
-    fp8 = args.workload in TREE_FP8_WORKLOADS
-    requests, hq, hkv, d, n_cand, lo, hi = TREE_WORKLOADS[TREE_FP8_WORKLOADS.get(args.workload, args.workload)]
-    k_rows = 16
-    q_len = n_cand * k_rows
+def tree_inputs(workload: str):
+    """Seeded CPU draw of a token-pool workload, in a fixed order: lengths, the pool slots
+    (a permutation), the queries (requests, n_cand x 16, heads, head_dim) and the K and V
+    pools (rounded to e4m3 for the fp8 workloads). Returns (lens, page table, q, k pool,
+    v pool)."""
+    fp8 = workload in TREE_FP8_WORKLOADS
+    requests, hq, hkv, d, n_cand, lo, hi = TREE_WORKLOADS[TREE_FP8_WORKLOADS.get(workload, workload)]
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(lo, hi + 1, (requests,), generator=g)
     ctx = int(lens.sum())
@@ -1024,12 +1022,25 @@ def run_tree(args, dev) -> dict:
     for b in range(requests):
         pt[b, :int(lens[b])] = slots[o:o + int(lens[b])]
         o += int(lens[b])
-    q = torch.randn(requests, q_len, hq, d, generator=g).bfloat16().to(dev)
+    q = torch.randn(requests, n_cand * 16, hq, d, generator=g).bfloat16()
     kb = torch.randn(ctx, hkv, d, generator=g).bfloat16()
     vb = torch.randn(ctx, hkv, d, generator=g).bfloat16()
     if fp8:  # e4m3 pools (round to nearest even, saturating at 448)
         kb, vb = (x.float().clamp(-448.0, 448.0).to(torch.float8_e4m3fn) for x in (kb, vb))
-    kb, vb = kb.to(dev), vb.to(dev)
+    return lens, pt, q, kb, vb
+
+
+def run_tree(args, dev) -> dict:
+    """One call = flashmap_sglang::paged_cross_attention of every request's candidates
+    side by side: query packing, the split-KV stream and the combine."""
+    from flashmap_amd import ops
+
+    fp8 = args.workload in TREE_FP8_WORKLOADS
+    requests, hq, hkv, d, n_cand, lo, hi = TREE_WORKLOADS[TREE_FP8_WORKLOADS.get(args.workload, args.workload)]
+    q_len = n_cand * 16
+    lens, pt, q, kb, vb = tree_inputs(args.workload)
+    ctx = int(lens.sum())
+    q, kb, vb = q.to(dev), kb.to(dev), vb.to(dev)
     lens_d, pt_d = lens.to(dev, torch.int32), pt.to(dev)
     plan = ops.attention_plan(lens_d)
     out = torch.empty_like(q)

@@ -8,11 +8,14 @@ the float32 oracle (max-abs 2e-2, mean-abs 2e-3 on the bf16 outputs):
   prologue fused into the contiguous attention call;
 - C2 at its full size: contiguous batch 1 x 2048 positions, 32 q / 8 KV heads, head_dim
   128, fused prologue, query positions 2048 + 0..15;
-- C3 (batch 64, contexts U[256, 8192]), C4 (batch 8 x 32768) and C5 (GQA 5, batch 32,
-  U[1024, 8192]): exactly the call bench.py times -- the query prologue fused, the step
+- C3 (batch 64, contexts U[256, 8192]), C4 (batch 8 x 32768), C5 (GQA 5, batch 32,
+  U[1024, 8192]) and R8B (MHA 16/16, batch 64, U[256, 8192]; its 1024 units take the query
+  pass): exactly the call bench.py times -- the query prologue fused, the step
   plan computed once and passed in, the paged op over the cache the context writer
   filled -- with every sequence of the batch checked against the oracle's prologue,
-  block-table gather and attention; and C3's call on an e4m3 cache the same way.
+  block-table gather and attention; and C3's call on an e4m3 cache the same way;
+- the SGLang drafter's call on token pools at C3's shape (bf16 and e4m3 pools), every
+  request against the oracle's gather and attention.
 """
 
 import pytest
@@ -113,7 +116,8 @@ def _bench_call(dev, workload, fp8=False):
     return inp, table, qpos, cache, out
 
 
-@pytest.mark.parametrize("workload", ["c3-qwen3-8b-paged-b64", "c4-qwen3-8b-long-b8", "c5-27b-gqa5-b32"])
+@pytest.mark.parametrize("workload", [
+    "c3-qwen3-8b-paged-b64", "c4-qwen3-8b-long-b8", "c5-27b-gqa5-b32", "r8b-mha-b64"])
 def test_bench_call_every_sequence(dev, workload):
     print(f"bench call {workload}", flush=True)
     inp, table, qpos, cache, out = _bench_call(dev, workload)
@@ -158,3 +162,41 @@ def test_bench_call_every_sequence_e4m3(dev):
         worst = max(worst, err.max().item())
     assert out.shape == (batch * k_rows, hq, d)
     print(f"c3 e4m3: {batch} sequences, worst max-abs {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("workload", ["c3shape-sglang-pool-b64", "c3shape-sglang-pool-b64-fp8"])
+def test_token_pool_bench_call_every_request(dev, workload):
+    """The SGLang drafter's cross-attention at C3's shape as bench.py times it
+    (``bench.tree_inputs``: 64 requests, contexts U[256, 8192] at permuted slots of
+    (pool, 8, 128) pools, 16 rows x 32 heads each, the step plan passed in): every request
+    against the oracle's gather and attention. e4m3 pools: the queries quantized per
+    (request, query head) by the oracle (the bits the call's own are pinned to), the pools
+    dequantized."""
+    import bench
+
+    print(f"bench call {workload}", flush=True)
+    ops = _ops()
+    lens, pt, q, kb, vb = bench.tree_inputs(workload)
+    fp8 = kb.dtype == torch.float8_e4m3fn
+    lens_d = lens.to(dev, torch.int32)
+    call = ops.block_attention_token_paged_fp8 if fp8 else ops.block_attention_token_paged
+    out = call(q.to(dev), kb.to(dev), vb.to(dev), lens_d, pt.to(dev), plan=ops.attention_plan(lens_d))
+    torch.cuda.synchronize()
+    requests, q_len, hq, d = q.shape
+    if fp8:
+        q8, qs = ref.quantize_query_per_head(q)
+        qd = q8.float() * qs[:, None, :, None]
+        kb, vb = kb.view(torch.uint8), vb.view(torch.uint8)  # gathered as bytes, then widened
+    else:
+        qd = q.float()
+    out = out.cpu().float()
+    worst = 0.0
+    for b in range(requests):
+        rows = pt[b, :int(lens[b])].long()
+        k, v = kb[rows], vb[rows]
+        if fp8:
+            k, v = k.view(torch.float8_e4m3fn), v.view(torch.float8_e4m3fn)
+        want = ref.attention(qd[b].transpose(0, 1), k.float().transpose(0, 1), v.float().transpose(0, 1), d ** -0.5)
+        err = check_close(out[b], want.transpose(0, 1))
+        worst = max(worst, err.max().item())
+    print(f"{workload}: {requests} requests, worst max-abs {worst:.3e}", flush=True)
