@@ -1107,6 +1107,35 @@ def tree_cpu_baseline(q, kb, vb, lens, pt, budget_s, fp8: bool = False) -> dict:
     return rec
 
 
+def verify_inputs(workload: str):
+    """Seeded CPU draw of a verify workload, in a fixed order: lengths, the context's pool
+    slots (a permutation), the queries, the verify tokens' keys and values, then the pools'
+    rows (drawn in slot order, 32768 at a time). Returns (lens, q, k_ext, v_ext, key pool,
+    value pool, kv_indptr, kv_indices, custom mask or None)."""
+    batch, hq, hkv, d, length, lo, hi, mask = VERIFY_WORKLOADS[workload]
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(lo, hi + 1, (batch,), generator=g)
+    ctx = int(lens.sum())
+    slots = torch.randperm(ctx, generator=g).to(torch.int32)
+    q = torch.randn(batch * length, hq, d, generator=g).bfloat16()
+    k_ext = torch.randn(batch * length, hkv, d, generator=g).bfloat16()
+    v_ext = torch.randn(batch * length, hkv, d, generator=g).bfloat16()
+    kb = torch.empty(ctx, hkv, d, dtype=torch.bfloat16)
+    vb = torch.empty_like(kb)
+    chunk = 1 << 15
+    for s in range(0, ctx, chunk):  # bounded fp32 temporaries
+        e = min(ctx, s + chunk)
+        kb[slots[s:e].long()] = torch.randn(e - s, hkv, d, generator=g).bfloat16()
+        vb[slots[s:e].long()] = torch.randn(e - s, hkv, d, generator=g).bfloat16()
+    indptr = torch.zeros(batch + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    cmask = None
+    if mask == "qlen":
+        tril = torch.ones(length, length, dtype=torch.bool).tril()
+        cmask = tril.reshape(-1).repeat(batch)
+    return lens, q, k_ext, v_ext, kb, vb, indptr, slots, cmask
+
+
 def run_verify(args, dev) -> dict:
     """One call = fm_verify_attention over the batch: plan, query packing, the split-KV
     stream of every request's context, and the combine that attends the verify tokens
@@ -1116,27 +1145,9 @@ def run_verify(args, dev) -> dict:
     from flashmap_amd import _native, ops
 
     batch, hq, hkv, d, length, lo, hi, mask = VERIFY_WORKLOADS[args.workload]
-    g = torch.Generator().manual_seed(0)
-    lens = torch.randint(lo, hi + 1, (batch,), generator=g)
+    lens, q, k_ext, v_ext, kb, vb, indptr, indices, cmask = (
+        x.to(dev) if isinstance(x, torch.Tensor) and i > 0 else x for i, x in enumerate(verify_inputs(args.workload)))
     ctx = int(lens.sum())
-    slots = torch.randperm(ctx, generator=g).to(torch.int32)
-    q = torch.randn(batch * length, hq, d, generator=g).bfloat16().to(dev)
-    k_ext = torch.randn(batch * length, hkv, d, generator=g).bfloat16().to(dev)
-    v_ext = torch.randn(batch * length, hkv, d, generator=g).bfloat16().to(dev)
-    kb = torch.empty(ctx, hkv, d, dtype=torch.bfloat16, device=dev)
-    vb = torch.empty_like(kb)
-    chunk = 1 << 15
-    for s in range(0, ctx, chunk):  # bounded fp32 temporaries
-        e = min(ctx, s + chunk)
-        kb[slots[s:e].long().to(dev)] = torch.randn(e - s, hkv, d, generator=g).bfloat16().to(dev)
-        vb[slots[s:e].long().to(dev)] = torch.randn(e - s, hkv, d, generator=g).bfloat16().to(dev)
-    indptr = torch.zeros(batch + 1, dtype=torch.int32)
-    indptr[1:] = torch.cumsum(lens, 0).to(torch.int32)
-    indptr, indices = indptr.to(dev), slots.to(dev)
-    cmask = None
-    if mask == "qlen":
-        tril = torch.ones(length, length, dtype=torch.bool).tril()
-        cmask = tril.reshape(-1).repeat(batch).to(dev)
     out = torch.empty_like(q)
 
     def call():

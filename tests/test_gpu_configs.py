@@ -15,7 +15,9 @@ the float32 oracle (max-abs 2e-2, mean-abs 2e-3 on the bf16 outputs):
   filled -- with every sequence of the batch checked against the oracle's prologue,
   block-table gather and attention; and C3's call on an e4m3 cache the same way;
 - the SGLang drafter's call on token pools at C3's shape (bf16 and e4m3 pools), every
-  request against the oracle's gather and attention.
+  request against the oracle's gather and attention;
+- the target verify call (64 requests x 17 chain tokens on a pool), every request against
+  the verify oracle.
 """
 
 import pytest
@@ -200,3 +202,30 @@ def test_token_pool_bench_call_every_request(dev, workload):
         err = check_close(out[b], want.transpose(0, 1))
         worst = max(worst, err.max().item())
     print(f"{workload}: {requests} requests, worst max-abs {worst:.3e}", flush=True)
+
+
+def test_verify_bench_call_every_request(dev):
+    """The target verify call as bench.py times it (``bench.verify_inputs`` of
+    verify-qwen3-8b-chain-b64: 64 requests x 17 chain tokens, 32/8 heads, contexts
+    U[256, 8192] at permuted slots of (pool, 8, 128) pools, causal among the verify tokens):
+    every request against the verify oracle on its gathered context."""
+    import bench
+
+    print("bench call verify-qwen3-8b-chain-b64", flush=True)
+    ops = _ops()
+    lens, q, k_ext, v_ext, kb, vb, indptr, indices, cmask = bench.verify_inputs("verify-qwen3-8b-chain-b64")
+    assert cmask is None
+    length = q.shape[0] // len(lens)
+    out = ops.verify_attention(q.to(dev), k_ext.to(dev), v_ext.to(dev), kb.to(dev), vb.to(dev), indptr.to(dev),
+                               indices.to(dev), None, None, False, max_context=int(lens.max()))
+    out = out.cpu().float()
+    worst = 0.0
+    for b in range(len(lens)):
+        lo_, hi_ = int(indptr[b]), int(indptr[b + 1])
+        rows = indices[lo_:hi_].long()
+        tok = slice(b * length, (b + 1) * length)
+        want = ref.verify_attention(q[tok], k_ext[tok], v_ext[tok], kb[rows], vb[rows],
+                                    torch.tensor([0, hi_ - lo_], dtype=torch.int32), torch.arange(hi_ - lo_))
+        err = check_close(out[tok], want)
+        worst = max(worst, err.max().item())
+    print(f"verify: {len(lens)} requests, worst max-abs {worst:.3e}", flush=True)
