@@ -14,8 +14,8 @@ the float32 oracle (max-abs 2e-2, mean-abs 2e-3 on the bf16 outputs):
   plan computed once and passed in, the paged op over the cache the context writer
   filled -- with every sequence of the batch checked against the oracle's prologue,
   block-table gather and attention; and C3's call on an e4m3 cache the same way;
-- the SGLang drafter's call on token pools at C3's shape (bf16 and e4m3 pools), every
-  request against the oracle's gather and attention;
+- the SGLang drafter's call on token pools at C3's shape (bf16 and e4m3 pools) and the
+  tree-drafting calls, every request against the oracle's gather and attention;
 - the target verify call (64 requests x 17 chain tokens on a pool), every request against
   the verify oracle.
 """
@@ -166,12 +166,14 @@ def test_bench_call_every_sequence_e4m3(dev):
     print(f"c3 e4m3: {batch} sequences, worst max-abs {worst:.3e}", flush=True)
 
 
-@pytest.mark.parametrize("workload", ["c3shape-sglang-pool-b64", "c3shape-sglang-pool-b64-fp8"])
+@pytest.mark.parametrize("workload", ["c3shape-sglang-pool-b64", "c3shape-sglang-pool-b64-fp8", "tree-r8b-b4-n8",
+                                      "tree-r8b-b1-n32"])
 def test_token_pool_bench_call_every_request(dev, workload):
-    """The SGLang drafter's cross-attention at C3's shape as bench.py times it
-    (``bench.tree_inputs``: 64 requests, contexts U[256, 8192] at permuted slots of
-    (pool, 8, 128) pools, 16 rows x 32 heads each, the step plan passed in): every request
-    against the oracle's gather and attention. e4m3 pools: the queries quantized per
+    """The SGLang drafter's cross-attention on token pools as bench.py times it
+    (``bench.tree_inputs``; at C3's shape: 64 requests, contexts U[256, 8192] at permuted
+    slots of (pool, 8, 128) pools, 16 rows x 32 heads each; tree drafting: 4 requests x 8
+    candidates and 1 x 32, 16/16 heads, the candidates' rows side by side; the step plan
+    passed in): every request against the oracle's gather and attention. e4m3 pools: the queries quantized per
     (request, query head) by the oracle (the bits the call's own are pinned to), the pools
     dequantized."""
     import bench
