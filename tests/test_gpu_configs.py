@@ -17,7 +17,8 @@ the float32 oracle (max-abs 2e-2, mean-abs 2e-3 on the bf16 outputs):
 - the SGLang drafter's call on token pools at C3's shape (bf16 and e4m3 pools) and the
   tree-drafting calls, every request against the oracle's gather and attention;
 - the target verify call (64 requests x 17 chain tokens on a pool), every request against
-  the verify oracle.
+  the verify oracle;
+- C3 through the virtual context-cache layout (4 runs), bit-identical to the per-layer call.
 """
 
 import pytest
@@ -231,3 +232,38 @@ def test_verify_bench_call_every_request(dev):
         err = check_close(out[tok], want)
         worst = max(worst, err.max().item())
     print(f"verify: {len(lens)} requests, worst max-abs {worst:.3e}", flush=True)
+
+
+def test_virtual_layout_bench_call_equals_per_layer(dev):
+    """The virtual context-cache call as bench.py times it (c3-qwen3-8b-virtual-hpc3: C3's
+    draw written for 2 DiT layers into caches of 3 heads each, layer 1's 8 KV heads in 4
+    runs, flashmap/vllm/context_cache.py): the same bits as the per-layer call on a cache of
+    the layer's 8 heads, which test_bench_call_every_sequence checks against the oracle."""
+    import bench
+    from flashmap_amd import context_cache as cc
+
+    print("bench call c3-qwen3-8b-virtual-hpc3", flush=True)
+    ops = _ops()
+    _, hpc, layer = bench.VIRTUAL_WORKLOADS["c3-qwen3-8b-virtual-hpc3"]
+    inp, _, qpos, _, per_layer = _bench_call(dev, "c3-qwen3-8b-paged-b64")
+    hkv, d, k_rows, page = inp["hkv"], inp["d"], inp["k_rows"], inp["page"]
+    table = ref.rope_table(inp["hi"] + k_rows + 1, d, THETA)
+    rope = ops.rope_from_table(table.to(dev))
+    w = torch.ones(d, device=dev)
+    vplan = cc.ContextCachePlan(layer + 1, hkv, -(-(layer + 1) * hkv // hpc), hpc, True, "")
+    caches = [torch.zeros(inp["total"], hpc, page, 2 * d, dtype=torch.bfloat16, device=dev)
+              for _ in range(vplan.num_caches)]
+    c0 = caches[0]
+    ops.write_context_kv(inp["kv_pre"].to(dev).repeat(1, layer + 1, 1, 1, 1), inp["positions"].to(dev),
+                         inp["slots"].to(dev), w[None].expand(layer + 1, d).contiguous(), rope,
+                         torch.tensor([c.data_ptr() for c in caches], dtype=torch.int64, device=dev),
+                         (c0.stride(0), c0.stride(1), c0.stride(2), d), page, EPS, heads_per_cache=hpc)
+    runs = vplan.segments[layer]
+    assert len(runs) == 4
+    lens = inp["lens"].to(dev, torch.int32)
+    cu = (torch.arange(inp["batch"] + 1, dtype=torch.int32) * k_rows).to(dev)
+    pro = ops.Prologue(w, rope, qpos.to(dev), EPS)
+    got = ops.block_attention_paged_runs(inp["q_pre"].to(dev), caches, runs, cu, lens, inp["bt"].to(dev), k_rows,
+                                         inp["hi"], d ** -0.5, prologue=pro, plan=ops.attention_plan(lens))
+    torch.cuda.synchronize()
+    assert torch.equal(got, per_layer)
