@@ -55,3 +55,38 @@ def test_the_first_item_alone_when_even_it_exceeds_the_budget():
     rec = bench.cpu_timed(_fake(1e-4, weights, log), weights, "us/call", "items", budget_s=0.007, threads=1)
     assert log == [1] * 8  # the sample never drops below one item
     assert "first 1 of 3 items" in rec["sample"]
+
+
+def test_more_than_one_gpu_is_refused():
+    """``bench.py --gpus N`` for N above 1 exits with status 2 and says why, before it
+    touches a GPU (one GPU is what is measured)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    p = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=root)
+    assert p.returncode == 2
+    assert "GPU" in p.stderr + p.stdout
+
+
+def test_committed_traffic_records_are_consistent():
+    """Each committed calibrated-traffic record: the copy calibration gives the factors (a
+    1 GiB copy reads and writes 1 GiB), and the record's bytes per launch are the kernel's
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled by them; its commands name the
+    counter runs they came from."""
+    import json
+    from pathlib import Path
+
+    recs = sorted((Path(__file__).resolve().parents[1] / "profiles").glob("*.traffic.json"))
+    assert recs
+    for f in recs:
+        r = json.loads(f.read_text())
+        ff = r["copy_bytes"] / (r["copy_fetch_kib"] * 1024)
+        wf = r["copy_bytes"] / (r["copy_write_kib"] * 1024)
+        assert abs(ff - r["fetch_factor"]) < 1e-4 and abs(wf - r["write_factor"]) < 1e-4, f.name
+        want = r["fetch_kib_per_dispatch"] * 1024 * ff + r["write_kib_per_dispatch"] * 1024 * wf
+        assert abs(r["traffic_bytes"] - want) / want < 1e-6, f.name
+        assert any("--pmc FETCH_SIZE" in c and r["workload"] in c for c in r["commands"]), f.name
+        assert any("--pmc WRITE_SIZE" in c and r["workload"] in c for c in r["commands"]), f.name
