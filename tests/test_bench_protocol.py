@@ -90,3 +90,29 @@ def test_committed_traffic_records_are_consistent():
         assert abs(r["traffic_bytes"] - want) / want < 1e-6, f.name
         assert any("--pmc FETCH_SIZE" in c and r["workload"] in c for c in r["commands"]), f.name
         assert any("--pmc WRITE_SIZE" in c and r["workload"] in c for c in r["commands"]), f.name
+
+
+def test_committed_mfma_records_are_consistent():
+    """Each committed MFMA record: its utilisation is SQ_VALU_MFMA_BUSY_CYCLES over the
+    SIMDs' cycles (1024 SIMDs, SQ_CYCLES counted per 32 shader engines), its MFMA work
+    (MOPS x 512 flop) is the workload's algorithmic 4 K Hq D sum(L) to within 1 % (no
+    MFMA work is wasted beyond the padding of a unit's rows), and its TFLOP/s is that work
+    over the counted dispatches' mean duration."""
+    import json
+    import re
+    from pathlib import Path
+
+    algorithmic = {"c3-qwen3-8b-paged-b64": 4 * 16 * 32 * 128 * 245380,
+                   "c3-qwen3-8b-paged-b64-fp8": 4 * 16 * 32 * 128 * 245380,
+                   "c5-27b-gqa5-b32": 4 * 16 * 40 * 128 * 172058}
+    recs = sorted((Path(__file__).resolve().parents[1] / "profiles").glob("*.mfma.json"))
+    assert recs
+    for f in recs:
+        r = json.loads(f.read_text())
+        c = r["counters"]
+        util = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (r["simds"] * c["SQ_CYCLES"] / r["shader_engines"])
+        assert abs(util - r["util"]) < 1e-3, f.name
+        flop = (c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] + c["SQ_INSTS_VALU_MFMA_MOPS_F8"]) * 512
+        assert 1.0 <= flop / algorithmic[r["workload"]] < 1.01, f.name
+        tflops = float(re.search(r"([0-9.]+) TFLOP/s", r["derivation"]).group(1))
+        assert abs(tflops - flop / (r["mean_duration_us"] * 1e-6) / 1e12) < 0.1, f.name
