@@ -46,7 +46,8 @@ def test_value_scaled_to_the_whole_call():
     n = log[1]
     assert 1 <= n < len(weights) and log == [1] + [n] * 4
     # a call of the whole batch would sleep 80 ms; the sample's median, scaled by weight, says so
-    assert 80e3 <= rec["value"] <= 80e3 * 1.3
+    # (sleeps never end early; a loaded host may add to them)
+    assert 80e3 <= rec["value"] <= 80e3 * 1.6
 
 
 def test_the_first_item_alone_when_even_it_exceeds_the_budget():
